@@ -1,0 +1,550 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 quantized-linear hot path (one MI355X).
+
+Headline (``value``): Q4_0 x Q8_0 M=1 throughput in GB/s on BASELINE cfg3, the
+TinyLlama-1.1B-shaped decode step -- 22 layers x 7 linears (q, k, v, o, gate,
+up, down), each activation re-quantised to Q8_0 right before its GEMV, 545 MB
+of Q4_0 weights per step (beyond the 256 MB MALL, so every step streams HBM).
+A step is the 308 kernels (154 quantise + 154 GEMV) replayed as one HIP graph.
+
+Also reported on the same JSON line:
+  * ``roofline``      -- the Q4_0 linear kernel's achieved HBM GB/s from its own
+                          per-launch device time (hipExtLaunchKernel events);
+  * ``w8a8``          -- cfg4 dynamic-W8A8 prefill GEMMs (M=4096) in TOPS, whole
+                          operator and GEMM-only, with an int8-MFMA roofline;
+  * ``configs``       -- cfg0 (rotated over >= 512 MB of weight copies), cfg1, cfg2;
+  * ``cpu_baseline``  -- the NumPy oracle of the reference CPU path on this host.
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--legs decode,w8a8,cfg0,cfg1,cfg2,copy,cpu]
+Weights and activations are synthetic (seeded random, the BASELINE distributions).
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "qpu-xla-triton_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "Q4_0×Q8_0 GEMV GB/s (%HBM peak); W8A8 GEMM int8 TOPS (%MFMA peak)"
+PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
+PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POP/s
+TINYLLAMA_LAYER = (  # (name, K, N)
+    ("q", 2048, 2048),
+    ("k", 2048, 256),
+    ("v", 2048, 256),
+    ("o", 2048, 2048),
+    ("gate", 2048, 5632),
+    ("up", 2048, 5632),
+    ("down", 5632, 2048),
+)
+LAYERS = 22
+ROTATION_BYTES = 512 << 20
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def q4_linear_bytes(m: int, k: int, n: int) -> int:
+    """Algorithmic bytes of one Q4_0 x Q8_0 linear: weights + Q8_0 activation + fp32 output."""
+    return n * (k // 32) * 18 + m * (k // 32) * 34 + m * n * 4
+
+
+def parse_args() -> argparse.Namespace:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--legs", default="decode,w8a8,cfg0,cfg1,cfg2,copy,cpu")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of each CPU-baseline sample")
+    return ap.parse_args()
+
+
+class Runner:
+    """Prebuilt ctypes calls on one stream, replayable eagerly or as a captured HIP graph."""
+
+    def __init__(self, torch, stream) -> None:
+        from qpu_xla_amd import _lib
+
+        self.torch = torch
+        self.stream = stream
+        self.lib = _lib.load()
+        self._lib = _lib
+        self.calls: list[tuple[object, tuple]] = []
+        self.handle = ctypes.c_void_p(int(stream.cuda_stream))
+
+    def add(self, name: str, *args) -> None:
+        self.calls.append((getattr(self.lib, name), args))
+
+    def run(self) -> None:
+        for fn, args in self.calls:
+            rc = fn(*args)
+            if rc:
+                self._lib.check(rc)
+
+    def capture(self):
+        torch = self.torch
+        graph = torch.cuda.CUDAGraph()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=self.stream):
+            self.run()
+        torch.cuda.synchronize()
+        return graph
+
+    def timed_graph(self, graph, steps: int, warmup: int) -> tuple[float, float]:
+        """(wall ms per replay, event ms per replay), synchronised on both sides."""
+        torch = self.torch
+        with torch.cuda.stream(self.stream):
+            for _ in range(warmup):
+                graph.replay()
+            torch.cuda.synchronize()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0 = time.perf_counter()
+            start.record(self.stream)
+            for _ in range(steps):
+                graph.replay()
+            end.record(self.stream)
+            torch.cuda.synchronize()
+            wall = (time.perf_counter() - t0) * 1e3 / steps
+        return wall, start.elapsed_time(end) / steps
+
+    def kernel_times(self, repeats: int = 1) -> dict[str, list[float]]:
+        """Device time of every launch of ``repeats`` eager runs, grouped by kernel name."""
+        out: dict[str, list[float]] = {}
+        with self._lib.launch_timing() as timing:
+            for _ in range(repeats):
+                self.run()
+        for name, ms in timing.records:
+            out.setdefault(name, []).append(ms)
+        return out
+
+
+def _p(t) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _rs(t) -> int:
+    return int(t.stride(0)) * t.element_size()
+
+
+# --------------------------------------------------------------------- legs
+
+
+def leg_decode(torch, args) -> dict:
+    """cfg3: 22 x 7 Q4_0 linears at M=1, each preceded by its Q8_0 quantisation."""
+    from qpu_xla_amd.kernels.quantize import quantize_q4_0
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3)
+    stream = torch.cuda.Stream()
+    runner = Runner(torch, stream)
+    keep = []
+    bytes_step = 0
+    q4_bytes_launches = []
+    for _layer in range(LAYERS):
+        for _name, k, n in TINYLLAMA_LAYER:
+            w = torch.randn((n, k), generator=gen, device="cuda", dtype=torch.float32) * 0.02
+            wq = quantize_q4_0(w)
+            del w
+            x = torch.randn((1, k), generator=gen, device="cuda", dtype=torch.float32)
+            xq = torch.empty((1, k // 32, 34), dtype=torch.uint8, device="cuda")
+            y = torch.empty((1, n), dtype=torch.float32, device="cuda")
+            keep.append((wq, x, xq, y))
+            runner.add("qxt_quantize_q8_0", _p(x), _rs(x), _p(xq), _rs(xq), 1, k, runner.handle)
+            runner.add("qxt_ggml_q4_0_q8_0_linear", _p(xq), _rs(xq), _p(wq), _rs(wq), _p(y), _rs(y),
+                       1, k // 32, 0, 0, n, runner.handle)
+            b = q4_linear_bytes(1, k, n)
+            bytes_step += b
+            q4_bytes_launches.append(b)
+    torch.cuda.synchronize()
+    log(f"decode: {len(keep)} linears, {bytes_step / 1e6:.1f} MB per step")
+    runner.run()
+    torch.cuda.synchronize()
+    times = runner.kernel_times(repeats=2)
+    q4_times = times.get("q4_0_linear_kernel", [])
+    q8_times = times.get("q8_0_kernel", [])
+    graph = runner.capture()
+    wall_ms, event_ms = runner.timed_graph(graph, args.steps, args.warmup)
+    q4_avg_ms = float(np.mean(q4_times))
+    q4_avg_bytes = float(np.mean(q4_bytes_launches))
+    achieved = q4_avg_bytes / (q4_avg_ms * 1e-3) / 1e9
+    result = {
+        "bytes_per_step": bytes_step,
+        "ms_per_step_wall": wall_ms,
+        "ms_per_step_events": event_ms,
+        "gbs": bytes_step / (wall_ms * 1e-3) / 1e9,
+        "q4_linear_avg_us": q4_avg_ms * 1e3,
+        "q4_linear_avg_bytes": q4_avg_bytes,
+        "q4_linear_kernel_gbs": achieved,
+        "q4_linear_sum_us_per_step": float(np.sum(q4_times)) * 1e3 / 2,
+        "q8_0_avg_us": float(np.mean(q8_times)) * 1e3 if q8_times else None,
+        "launches_per_step": len(runner.calls),
+    }
+    del graph, keep
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return result
+
+
+def leg_rotated_q4(torch, args, rows: int, k: int, n: int, seed: int) -> dict:
+    """One Q4_0 linear shape, cycling through >= 512 MB of distinct weight copies."""
+    from qpu_xla_amd.kernels.quantize import quantize_q4_0, quantize_q8_0
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    per = n * (k // 32) * 18
+    copies = max(2, -(-ROTATION_BYTES // per))
+    stream = torch.cuda.Stream()
+    runner = Runner(torch, stream)
+    weights = []
+    for _ in range(copies):
+        w = torch.randn((n, k), generator=gen, device="cuda", dtype=torch.float32) * 0.02
+        weights.append(quantize_q4_0(w))
+        del w
+    x = torch.randn((rows, k), generator=gen, device="cuda", dtype=torch.float32)
+    xq = quantize_q8_0(x)
+    y = torch.empty((rows, n), dtype=torch.float32, device="cuda")
+    for wq in weights:
+        runner.add("qxt_ggml_q4_0_q8_0_linear", _p(xq), _rs(xq), _p(wq), _rs(wq), _p(y), _rs(y),
+                   rows, k // 32, 0, 0, n, runner.handle)
+    runner.run()
+    torch.cuda.synchronize()
+    times = runner.kernel_times(repeats=2)["q4_0_linear_kernel"]
+    graph = runner.capture()
+    wall_ms, _ = runner.timed_graph(graph, max(2, args.steps // 4), 2)
+    b = q4_linear_bytes(rows, k, n)
+    avg_ms = float(np.mean(times))
+    out = {
+        "shape": f"M={rows} K={k} N={n}",
+        "copies": copies,
+        "rotation_mb": copies * per / 1e6,
+        "bytes_per_launch": b,
+        "kernel_avg_us": avg_ms * 1e3,
+        "kernel_gbs": b / (avg_ms * 1e-3) / 1e9,
+        "kernel_frac_hbm": b / (avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+        "stream_us_per_launch": wall_ms * 1e3 / copies,
+        "stream_gbs": b * copies / (wall_ms * 1e-3) / 1e9,
+    }
+    del graph, weights
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
+def _w8a8_operands(torch, gen, m: int, k: int, n: int):
+    from qpu_xla_amd.quantization import quantize_per_output_channel_int8
+
+    x = torch.randn((m, k), generator=gen, device="cuda", dtype=torch.float32)
+    outliers = torch.randperm(k, generator=gen, device="cuda")[: max(1, round(0.001 * k))]
+    x[:, outliers] *= 20.0
+    w = torch.randn((n, k), generator=gen, device="cuda", dtype=torch.float32) * 0.02
+    weight = quantize_per_output_channel_int8(w)
+    del w
+    bias = torch.randn((n,), generator=gen, device="cuda", dtype=torch.float32) * 0.1
+    return x, weight, bias
+
+
+def leg_w8a8(torch, args) -> dict:
+    """cfg4: dynamic W8A8 prefill GEMMs at Llama-3-8B FFN shapes, M=4096."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(4)
+    shapes = {"gate_up": (4096, 4096, 14336), "down": (4096, 14336, 4096)}
+    result = {}
+    total_ops = 0
+    total_ms = 0.0
+    total_gemm_ms = 0.0
+    for label, (m, k, n) in shapes.items():
+        x, weight, bias = _w8a8_operands(torch, gen, m, k, n)
+        qa = torch.empty((m, k), dtype=torch.int8, device="cuda")
+        sa = torch.empty((m,), dtype=torch.float32, device="cuda")
+        y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        stream = torch.cuda.Stream()
+        runner = Runner(torch, stream)
+        runner.add("qxt_w8a8_linear", _p(x), _rs(x), _p(qa), _rs(qa), _p(sa), _p(weight.values),
+                   _rs(weight.values), _p(weight.scales), _p(bias), _p(y), _rs(y), m, n, k, 0, 0, runner.handle)
+        runner.run()
+        torch.cuda.synchronize()
+        times = runner.kernel_times(repeats=3)
+        graph = runner.capture()
+        wall_ms, event_ms = runner.timed_graph(graph, max(3, args.steps // 2), 2)
+        ops = 2 * m * n * k
+        gemm_ms = float(np.mean(times["w8a8_gemm_kernel"]))
+        quant_ms = float(np.mean(times["rows_int8_kernel"]))
+        result[label] = {
+            "shape": f"M={m} K={k} N={n}",
+            "operator_ms": wall_ms,
+            "operator_tops": ops / (wall_ms * 1e-3) / 1e12,
+            "gemm_ms": gemm_ms,
+            "gemm_tops": ops / (gemm_ms * 1e-3) / 1e12,
+            "gemm_frac_mfma": ops / (gemm_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS,
+            "row_quantise_ms": quant_ms,
+        }
+        total_ops += ops
+        total_ms += wall_ms
+        total_gemm_ms += gemm_ms
+        del graph, x, weight, bias, qa, sa, y
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    gemm_tops = total_ops / (total_gemm_ms * 1e-3) / 1e12
+    result["value"] = total_ops / (total_ms * 1e-3) / 1e12
+    result["unit"] = "TOPS"
+    result["roofline"] = {
+        "bound": "mfma",
+        "kernel": "w8a8_gemm_kernel",
+        "achieved": gemm_tops,
+        "peak": PEAK_INT8_TOPS,
+        "unit": "TFLOP/s",
+        "frac": gemm_tops / PEAK_INT8_TOPS,
+        "ops_per_launch": total_ops // 2,
+    }
+    return result
+
+
+def leg_cfg1(torch, args) -> dict:
+    """cfg1: W8A8 M=K=N=512 whole operator (launch-bound; parity case, reported only)."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(1)
+    m = k = n = 512
+    x = torch.randn((m, k), generator=gen, device="cuda", dtype=torch.float32)
+    from qpu_xla_amd.quantization import quantize_per_output_channel_int8
+
+    weight = quantize_per_output_channel_int8(torch.randn((n, k), generator=gen, device="cuda") * 0.05)
+    bias = torch.randn((n,), generator=gen, device="cuda") * 0.1
+    qa = torch.empty((m, k), dtype=torch.int8, device="cuda")
+    sa = torch.empty((m,), dtype=torch.float32, device="cuda")
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    runner = Runner(torch, torch.cuda.Stream())
+    for _ in range(32):
+        runner.add("qxt_w8a8_linear", _p(x), _rs(x), _p(qa), _rs(qa), _p(sa), _p(weight.values), _rs(weight.values),
+                   _p(weight.scales), _p(bias), _p(y), _rs(y), m, n, k, 0, 0, runner.handle)
+    runner.run()
+    times = runner.kernel_times()
+    graph = runner.capture()
+    wall_ms, _ = runner.timed_graph(graph, 10, 2)
+    return {
+        "shape": "M=K=N=512",
+        "operator_us": wall_ms * 1e3 / 32,
+        "gemm_kernel_us": float(np.mean(times["w8a8_gemm_kernel"])) * 1e3,
+        "quantise_kernel_us": float(np.mean(times["rows_int8_kernel"])) * 1e3,
+        "operator_tops": 2 * m * n * k / (wall_ms * 1e-3 / 32) / 1e12,
+    }
+
+
+def leg_copy(torch) -> dict:
+    """Device-to-device copy ceiling (reads + writes) for context next to the 8 TB/s spec."""
+    nbytes = 1 << 30
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(10):
+        dst.copy_(src)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / 10
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"bytes": 2 * nbytes, "gbs": 2 * nbytes / (ms * 1e-3) / 1e9}
+
+
+def cpu_baseline_q4(budget_s: float) -> dict:
+    """The NumPy oracle (reference CPU path) on the cfg3 decode step, bounded by ``budget_s``."""
+    import oracle
+
+    rng = np.random.default_rng(3)
+    done_bytes = 0
+    done = 0
+    elapsed = 0.0
+    linears = [(k, n) for _ in range(LAYERS) for (_, k, n) in TINYLLAMA_LAYER]
+    for k, n in linears:
+        w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+        wq = oracle.quantize_q4_0_blocks(w)  # weight preparation: outside the timed region
+        x = rng.standard_normal((1, k), dtype=np.float32)
+        t0 = time.perf_counter()
+        xq = oracle.quantize_q8_0_blocks(x)
+        oracle.q4_0_q8_0_reference(xq, wq)
+        elapsed += time.perf_counter() - t0
+        done_bytes += q4_linear_bytes(1, k, n)
+        done += 1
+        if elapsed >= budget_s:
+            break
+    return {
+        "value": done_bytes / elapsed / 1e9,
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{done} of 154 cfg3 linears (Q8_0 quantise + Q4_0xQ8_0 oracle, NumPy single thread), "
+        f"{done_bytes / 1e6:.1f} MB in {elapsed:.2f} s",
+    }
+
+
+def cpu_baseline_w8a8(budget_s: float) -> dict:
+    """NumPy oracle of the dynamic W8A8 linear on a row sample of cfg4 gate/up (int32 matmul is not BLAS)."""
+    import oracle
+
+    rng = np.random.default_rng(4)
+    k, n = 4096, 14336
+    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    qw, sw = oracle.quantize_per_output_channel_int8(w)
+    qw32 = qw.astype(np.int32)
+    bias = (rng.standard_normal(n, dtype=np.float32) * np.float32(0.1)).astype(np.float32)
+    rows = 0
+    elapsed = 0.0
+    while elapsed < budget_s and rows < 64:
+        x = rng.standard_normal((8, k), dtype=np.float32)
+        t0 = time.perf_counter()
+        qa, sa = oracle.quantize_rows_int8(x)
+        acc = qa.astype(np.int32) @ qw32.T
+        oracle.dequantize_epilogue(acc, sa, sw, bias)
+        elapsed += time.perf_counter() - t0
+        rows += 8
+    return {
+        "value": 2 * rows * n * k / elapsed / 1e12,
+        "unit": "TOPS",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{rows} of 4096 rows of cfg4 gate/up (K=4096, N=14336), NumPy int32 matmul, {elapsed:.2f} s",
+    }
+
+
+def host_info() -> dict:
+    info = {"cpu_count": os.cpu_count()}
+    try:
+        info["affinity"] = len(os.sched_getaffinity(0))
+    except AttributeError:
+        pass
+    for var in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS"):
+        info[var] = os.environ.get(var)
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    info["cpu_model"] = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return info
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(
+            "bench.py measures one GPU only: the quantized-linear path is benchmarked per device "
+            "(multi-GPU sharding is a design note, not a measured configuration); run with --gpus 1",
+            file=sys.stderr,
+        )
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        return 1
+    from qpu_xla_amd import _lib
+
+    info = _lib.device_info()
+    legs = set(args.legs.split(","))
+    device = {
+        "arch": info.arch.decode(),
+        "compute_units": info.compute_units,
+        "clock_mhz": info.clock_khz / 1e3,
+        "hbm_gib": info.total_memory / 2**30,
+    }
+    log(f"device {device}")
+    out: dict = {}
+    if "decode" in legs:
+        log("leg decode (cfg3)")
+        out["decode"] = leg_decode(torch, args)
+        log(f"decode: {out['decode']}")
+    if "cfg0" in legs:
+        log("leg cfg0 rotated")
+        out["cfg0"] = leg_rotated_q4(torch, args, 1, 2048, 5632, 0)
+        log(f"cfg0: {out['cfg0']}")
+    if "cfg2" in legs:
+        log("leg cfg2 rotated")
+        out["cfg2"] = [leg_rotated_q4(torch, args, 4, 4096, 11008, 2), leg_rotated_q4(torch, args, 4, 4096, 4096, 2)]
+        log(f"cfg2: {out['cfg2']}")
+    if "w8a8" in legs:
+        log("leg w8a8 (cfg4)")
+        out["w8a8"] = leg_w8a8(torch, args)
+        log(f"w8a8: {out['w8a8']}")
+    if "cfg1" in legs:
+        log("leg cfg1")
+        out["cfg1"] = leg_cfg1(torch, args)
+        log(f"cfg1: {out['cfg1']}")
+    if "copy" in legs:
+        out["copy"] = leg_copy(torch)
+        log(f"copy: {out['copy']}")
+    cpu = None
+    cpu_w8a8 = None
+    if "cpu" in legs:
+        log("cpu baseline (NumPy oracle)")
+        cpu = cpu_baseline_q4(args.cpu_seconds)
+        cpu_w8a8 = cpu_baseline_w8a8(args.cpu_seconds)
+        cpu["host"] = host_info()
+        log(f"cpu: {cpu} / {cpu_w8a8}")
+
+    decode = out.get("decode")
+    line = {
+        "metric": METRIC,
+        "value": decode["gbs"] if decode else None,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": decode["ms_per_step_wall"] if decode else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 dot4 (Q4_0 x Q8_0) -> int32 block dots -> fp32",
+        "data": "synthetic (seeded N(0,0.02) weights quantised to Q4_0, N(0,1) activations)",
+        "config": {
+            "workload": "cfg3: TinyLlama-1.1B decode step, 22 layers x 7 Q4_0xQ8_0 linears "
+            "(q/o 2048x2048, k/v 2048->256, gate/up 2048->5632, down 5632->2048), M=1, "
+            "Q8_0 re-quantisation before each linear, one HIP graph per step",
+            "bytes_per_step": decode["bytes_per_step"] if decode else None,
+            "frac_hbm_peak": decode["gbs"] / PEAK_HBM_GBS if decode else None,
+        },
+        "roofline": (
+            {
+                "bound": "hbm",
+                "kernel": "q4_0_linear_kernel",
+                "achieved": decode["q4_linear_kernel_gbs"],
+                "peak": PEAK_HBM_GBS,
+                "unit": "GB/s",
+                "frac": decode["q4_linear_kernel_gbs"] / PEAK_HBM_GBS,
+                "traffic": None,
+                "bytes_per_launch": decode["q4_linear_avg_bytes"],
+                "avg_launch_us": decode["q4_linear_avg_us"],
+            }
+            if decode
+            else None
+        ),
+        "cpu_baseline": cpu,
+        "w8a8": out.get("w8a8"),
+        "w8a8_cpu_baseline": cpu_w8a8,
+        "decode": decode,
+        "configs": {key: out[key] for key in ("cfg0", "cfg1", "cfg2") if key in out},
+        "copy_ceiling_gbs": out.get("copy", {}).get("gbs"),
+        "device": device,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,54 @@
+"""CPU oracle for the quantized-linear hot path (TEST INFRASTRUCTURE ONLY).
+
+This package is a NumPy restatement of the reference's CPU algorithms for the
+Q4_0 x Q8_0 block-dot linear, the Q8_0 / Q4_0 / per-row int8 quantisers and
+the dynamic W8A8 int8 GEMM with its dequant + bias epilogue.  Every function
+cites the reference file:line it follows (paths are relative to the
+``yiannisha/qpu-xla-triton`` source tree).
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline
+leg may import it, and only as the checker / the timed CPU baseline.  The
+product package (``qpu_xla_amd``) never imports or calls it: the product
+path is the HIP library and fails loudly when that library is missing.
+
+Pinning status (what each function is checked against, in ``tests/``):
+
+* block codecs: round trips plus the reference's extreme-value cases
+  (tests/test_qpu_xla_ggml_q4_0.py:25-44 in the reference).
+* ``q4_0_q8_0_reference``: closed-form integer KATs of the native smokes
+  (integrations/llama_cpp/tests/qpu_llama_q4_0_smoke.c:15-36,
+  qpu_llama_q4_0_m4_smoke.c:17-40), exact power-of-two-scale cases, and a
+  float64 dequantised brute force.
+* ``quantize_q8_0_*``: invariants (|q| <= 127, absmax maps to +-127, fp16
+  RNE scale) and exact half-way ties that separate ``rint`` from ``round``.
+* W8A8: closed-form KAT (qpu_llama_w8a8_smoke.c:58-66), int64 brute force,
+  quantiser invariants including the 1/127 scale floor.
+* ``quantize_q4_0_blocks``: PARITY UNPINNED against upstream ggml
+  ``quantize_row_q4_0`` (ggml is not vendored in the reference); only the
+  BASELINE formula's invariants are checked.
+"""
+
+from oracle.ggml import (  # noqa: F401
+    Q4_0_BLOCK_BYTES,
+    Q8_0_BLOCK_BYTES,
+    QK,
+    pack_q4_0_blocks,
+    pack_q8_0_blocks,
+    q4_0_q8_0_block_dots,
+    q4_0_q8_0_reference,
+    quantize_q4_0_blocks,
+    quantize_q8_0_blocks,
+    quantize_q8_0_split,
+    unpack_q4_0_blocks,
+    unpack_q8_0_blocks,
+)
+from oracle.w8a8 import (  # noqa: F401
+    SCALE_FLOOR,
+    dequantize_epilogue,
+    int8_gemm_i32,
+    pack_int8_gemm_operands,
+    pack_int8_quads,
+    quantize_per_output_channel_int8,
+    quantize_rows_int8,
+    w8a8_linear_reference,
+)

@@ -1,0 +1,197 @@
+"""NumPy oracle for the GGML Q4_0 / Q8_0 block formats and their block-dot linear.
+
+TEST INFRASTRUCTURE ONLY -- see ``oracle/__init__.py`` for who may import it.
+
+Block formats (reference ``src/qpu_xla/kernels/ggml_q4_0.py:21-25``):
+
+* Q4_0, 18 bytes: little-endian fp16 scale ``d``, then 16 bytes whose byte
+  ``j`` holds element ``j`` in the low nibble and element ``j + 16`` in the
+  high nibble; value = code - 8.
+* Q8_0, 34 bytes: little-endian fp16 scale ``d``, then 32 signed bytes.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+QK = 32
+Q4_0_BLOCK_BYTES = 18
+Q8_0_BLOCK_BYTES = 34
+
+
+def pack_q4_0_blocks(scales: np.ndarray, codes: np.ndarray) -> np.ndarray:
+    """Pack explicit 0..15 codes plus fp16 scales into 18-byte Q4_0 blocks.
+
+    Follows ``src/qpu_xla/kernels/ggml_q4_0.py:28-40``.
+    """
+    scales = np.asarray(scales, dtype=np.float16)
+    codes = np.asarray(codes)
+    if codes.shape != (*scales.shape, QK):
+        raise ValueError("Q4_0 codes must have shape scales.shape + (32,)")
+    if np.any((codes < 0) | (codes > 15)):
+        raise ValueError("Q4_0 codes must lie in 0..15")
+    out = np.empty((*scales.shape, Q4_0_BLOCK_BYTES), dtype=np.uint8)
+    out[..., 0:2] = scales.astype("<f2").view(np.uint8).reshape(*scales.shape, 2)
+    low = codes[..., :16].astype(np.uint8)
+    high = codes[..., 16:].astype(np.uint8)
+    out[..., 2:] = low | (high << 4)
+    return out
+
+
+def pack_q8_0_blocks(scales: np.ndarray, values: np.ndarray) -> np.ndarray:
+    """Pack signed bytes plus fp16 scales into 34-byte Q8_0 blocks.
+
+    Follows ``src/qpu_xla/kernels/ggml_q4_0.py:43-55``.
+    """
+    scales = np.asarray(scales, dtype=np.float16)
+    values = np.asarray(values)
+    if values.shape != (*scales.shape, QK):
+        raise ValueError("Q8_0 values must have shape scales.shape + (32,)")
+    if np.any((values < -128) | (values > 127)):
+        raise ValueError("Q8_0 values must lie in -128..127")
+    out = np.empty((*scales.shape, Q8_0_BLOCK_BYTES), dtype=np.uint8)
+    out[..., 0:2] = scales.astype("<f2").view(np.uint8).reshape(*scales.shape, 2)
+    out[..., 2:] = values.astype(np.int8).view(np.uint8)
+    return out
+
+
+def _fp16_field(blocks: np.ndarray) -> np.ndarray:
+    raw = np.ascontiguousarray(blocks[..., 0:2])
+    return raw.view("<f2").reshape(blocks.shape[:-1])
+
+
+def unpack_q4_0_blocks(blocks: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Decode Q4_0 blocks to (fp32 scales, int8 values in -8..7).
+
+    Follows ``src/qpu_xla/kernels/ggml_q4_0.py:58-68``.
+    """
+    blocks = np.asarray(blocks)
+    if blocks.dtype != np.uint8 or blocks.ndim < 1 or blocks.shape[-1] != Q4_0_BLOCK_BYTES:
+        raise ValueError("Q4_0 blocks must be uint8 with a trailing extent of 18")
+    scales = _fp16_field(blocks).astype(np.float32)
+    qs = blocks[..., 2:]
+    values = np.empty((*blocks.shape[:-1], QK), dtype=np.int8)
+    values[..., :16] = (qs & 0x0F).astype(np.int8) - 8
+    values[..., 16:] = (qs >> 4).astype(np.int8) - 8
+    return scales, values
+
+
+def unpack_q8_0_blocks(blocks: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Decode Q8_0 blocks to (fp32 scales, int8 values).
+
+    Follows ``src/qpu_xla/kernels/ggml_q4_0.py:71-78``.
+    """
+    blocks = np.asarray(blocks)
+    if blocks.dtype != np.uint8 or blocks.ndim < 1 or blocks.shape[-1] != Q8_0_BLOCK_BYTES:
+        raise ValueError("Q8_0 blocks must be uint8 with a trailing extent of 34")
+    scales = _fp16_field(blocks).astype(np.float32)
+    values = np.ascontiguousarray(blocks[..., 2:]).view(np.int8)
+    return scales, values
+
+
+def _check_linear_operands(activation_blocks: np.ndarray, weight_blocks: np.ndarray) -> None:
+    if activation_blocks.ndim != 3 or weight_blocks.ndim != 3:
+        raise ValueError("activation and weight blocks must both be rank three")
+    if activation_blocks.shape[2] != Q8_0_BLOCK_BYTES or weight_blocks.shape[2] != Q4_0_BLOCK_BYTES:
+        raise ValueError("activation blocks must be Q8_0 (34 B) and weight blocks Q4_0 (18 B)")
+    if activation_blocks.shape[1] != weight_blocks.shape[1]:
+        raise ValueError("activation and weight reduction block counts differ")
+
+
+def q4_0_q8_0_block_dots(activation_blocks: np.ndarray, weight_blocks: np.ndarray) -> np.ndarray:
+    """Exact int32 per-block dots ``dot[m, n, b] = sum_k a[m,b,k] * (code[n,b,k] - 8)``.
+
+    These are the integer terms of ``src/qpu_xla/kernels/ggml_q4_0.py:96``.
+    Shapes: activation u8 [M, B, 34], weight u8 [N, B, 18] -> int32 [M, N, B].
+    """
+    _check_linear_operands(activation_blocks, weight_blocks)
+    _, a = unpack_q8_0_blocks(activation_blocks)
+    _, w = unpack_q4_0_blocks(weight_blocks)
+    return np.einsum("mbk,nbk->mnb", a.astype(np.int32), w.astype(np.int32)).astype(np.int32)
+
+
+def q4_0_q8_0_reference(activation_blocks: np.ndarray, weight_blocks: np.ndarray) -> np.ndarray:
+    """Q4_0 x Q8_0 linear: ``y[m, n] = sum_b fl32(fl32(dot * dw[n,b]) * da[m,b])``.
+
+    Follows ``src/qpu_xla/kernels/ggml_q4_0.py:81-100`` op for op: per block
+    an exact int32 dot, converted to fp32, multiplied by the weight scale,
+    then by the activation scale, and added to an fp32 accumulator in block
+    order ``((0 + c_0) + c_1) + ...``.  NumPy float32 arithmetic performs
+    each multiply and add with its own rounding (no fused multiply-add).
+    """
+    _check_linear_operands(activation_blocks, weight_blocks)
+    a_scale, a = unpack_q8_0_blocks(activation_blocks)
+    w_scale, w = unpack_q4_0_blocks(weight_blocks)
+    rows, blocks = a_scale.shape
+    outputs = w_scale.shape[0]
+    result = np.zeros((rows, outputs), dtype=np.float32)
+    for b in range(blocks):
+        dots = a[:, b].astype(np.int32) @ w[:, b].astype(np.int32).T
+        term = dots.astype(np.float32) * w_scale[None, :, b]
+        term *= a_scale[:, b, None]
+        result += term
+    return result
+
+
+def quantize_q8_0_split(values: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Quantise fp32 rows to Q8_0: (fp16 scale bits u16 [M, K/32], int8 codes [M, K]).
+
+    Follows the repository's own quantiser,
+    ``examples/benchmark_llama_cpp_qpu_persistent_q4.py:42-53``:
+    ``d = fl32(absmax / 127)``; ``inv = fl32(1 / d)`` (0 when d == 0);
+    ``q = clip(rint(fl32(x * inv)), -127, 127)`` with round-half-even;
+    ``d`` stored as fp16 with round-to-nearest-even.
+    """
+    values = np.asarray(values, dtype=np.float32)
+    if values.ndim != 2 or values.shape[1] % QK:
+        raise ValueError("Q8_0 quantisation needs rank-2 rows whose length is a multiple of 32")
+    rows, columns = values.shape
+    grouped = values.reshape(rows, columns // QK, QK)
+    scales = np.max(np.abs(grouped), axis=2).astype(np.float32) / np.float32(127.0)
+    inverse = np.zeros_like(scales)
+    np.divide(np.float32(1.0), scales, out=inverse, where=scales != 0.0)
+    codes = np.clip(np.rint(grouped * inverse[..., None]), -127, 127).astype(np.int8)
+    return (
+        np.ascontiguousarray(scales.astype(np.float16).view(np.uint16)),
+        np.ascontiguousarray(codes.reshape(rows, columns)),
+    )
+
+
+def quantize_q8_0_blocks(values: np.ndarray) -> np.ndarray:
+    """Quantise fp32 rows [M, K] into native Q8_0 blocks u8 [M, K/32, 34] (same math as above)."""
+    scale_bits, codes = quantize_q8_0_split(values)
+    rows, columns = codes.shape
+    out = np.empty((rows, columns // QK, Q8_0_BLOCK_BYTES), dtype=np.uint8)
+    out[..., 0:2] = scale_bits.astype("<u2").view(np.uint8).reshape(rows, columns // QK, 2)
+    out[..., 2:] = codes.reshape(rows, columns // QK, QK).view(np.uint8)
+    return out
+
+
+def quantize_q4_0_blocks(weights: np.ndarray) -> np.ndarray:
+    """Quantise fp32 rows [N, K] into native Q4_0 blocks u8 [N, K/32, 18].
+
+    PARITY UNPINNED against upstream ggml: the reference has no Python Q4_0
+    quantiser and only calls ggml's ``quantize_row_q4_0`` from native tests
+    (``integrations/llama_cpp/tests/qpu_ggml_backend_smoke.cpp:119``; llama.cpp
+    pinned at 91d2fc387529940230555abd297a8b5e99737d3f, not vendored).  This
+    restates ggml's published reference quantiser, which implements the
+    BASELINE formula ``d = signed_absmax / -8``, ``q = clamp(round(x/d) + 8, 0, 15)``:
+
+    * ``max`` = the first element of largest magnitude (+0.0 for an all-zero block),
+    * ``d = fl32(max / -8)``, ``id = fl32(1 / d)`` or 0 when d == 0,
+    * ``q = min(15, trunc(fl32(fl32(x * id) + 8.5)))``, ``d`` stored as fp16 (RNE).
+    """
+    weights = np.asarray(weights, dtype=np.float32)
+    if weights.ndim != 2 or weights.shape[1] % QK:
+        raise ValueError("Q4_0 quantisation needs rank-2 rows whose length is a multiple of 32")
+    rows, columns = weights.shape
+    grouped = weights.reshape(rows, columns // QK, QK)
+    first = np.argmax(np.abs(grouped), axis=2)
+    signed_max = np.take_along_axis(grouped, first[..., None], axis=2)[..., 0]
+    signed_max = np.where(np.abs(signed_max) > 0, signed_max, np.float32(0.0)).astype(np.float32)
+    d = signed_max / np.float32(-8.0)
+    inverse = np.zeros_like(d)
+    np.divide(np.float32(1.0), d, out=inverse, where=d != 0.0)
+    shifted = (grouped * inverse[..., None]) + np.float32(8.5)
+    codes = np.minimum(np.trunc(shifted), 15).astype(np.uint8)
+    return pack_q4_0_blocks(d.astype(np.float16), codes)

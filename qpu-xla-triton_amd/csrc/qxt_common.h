@@ -1,0 +1,81 @@
+// Shared host/device helpers of the gfx950 quantized-linear library.
+#pragma once
+
+#include <hip/hip_ext.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "qxt_gfx950.h"
+
+namespace qxt {
+
+// ---------------------------------------------------------------- host side
+
+// Record `message` as the calling thread's last error and return `status`.
+int fail(int status, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// OK when no failure is injected for `point`, else the mapped status (with a message).
+int injected(uint32_t point);
+
+// Map the result of a kernel launch (hipGetLastError) to a status.
+int launch_status(const char *kernel_name);
+
+inline hipStream_t as_stream(void *stream) { return reinterpret_cast<hipStream_t>(stream); }
+
+inline bool aligned(const void *p, size_t bytes) {
+    return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
+}
+
+// Number of compute units of the current device (cached per device).
+int compute_units();
+
+// Per-launch timing (qxt_timing_begin/end): when enabled on the calling
+// thread, launches record device-side start/stop events.
+bool timing_enabled();
+void timing_events(hipEvent_t *start, hipEvent_t *stop);
+void timing_record(const char *kernel_name, hipEvent_t start, hipEvent_t stop);
+
+// Launch `kernel` on `stream`; every kernel of the library goes through here.
+template <typename... KArgs, typename... Args>
+int launch(const char *name, void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t lds, hipStream_t stream,
+           Args... args) {
+    if (timing_enabled()) {
+        hipEvent_t start = nullptr, stop = nullptr;
+        timing_events(&start, &stop);
+        hipExtLaunchKernelGGL(kernel, grid, block, static_cast<uint32_t>(lds), stream, start, stop, 0u,
+                              static_cast<KArgs>(args)...);
+        timing_record(name, start, stop);
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, static_cast<uint32_t>(lds), stream, static_cast<KArgs>(args)...);
+    }
+    return launch_status(name);
+}
+
+// -------------------------------------------------------------- device side
+
+constexpr int QK = 32;            // elements per GGML block
+constexpr int Q4_0_BYTES = 18;    // fp16 d + 16 nibble bytes
+constexpr int Q8_0_BYTES = 34;    // fp16 d + 32 int8
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
+    __half_raw raw;
+    raw.x = static_cast<unsigned short>(bits16 & 0xFFFFu);
+    return __half2float(__half(raw));
+}
+
+__device__ __forceinline__ uint32_t float_to_half_bits(float value) {
+    // Round-to-nearest-even conversion (v_cvt_f16_f32 under the default mode).
+    __half h = __float2half_rn(value);
+    __half_raw raw = static_cast<__half_raw>(h);
+    return raw.x;
+}
+
+// Signed 4 x int8 dot product accumulated into int32 (v_dot4_i32_i8).
+__device__ __forceinline__ int dot4(int a, int b, int c) {
+    return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+}  // namespace qxt

@@ -1,0 +1,207 @@
+"""Native GGML Q4_0 x Q8_0 linear on gfx950.
+
+Mirrors the operator surface of the reference's
+``src/qpu_xla/kernels/ggml_q4_0.py``: the same block constants and codec
+helpers, a ``supports_ggml_q4_0_q8_0_linear`` predicate, an executor that
+re-validates and checks the grid, and a ``Kernel`` constant submitted through
+``Queue.submit(kernel, (activation, weight, destination, wcol0, ocol0, ncols),
+grid=(ncols // 16, ceil(rows / 4), 1))``.  Tensors are torch tensors on the
+HIP device; the kernel writes only ``destination[:, ocol0:ocol0 + ncols]``.
+
+Differences from the reference contract, all widening it: any ``rows >= 1``
+(the reference QPU program needs 4 or a multiple of 16 and its native runtime
+replicates M=1 four times), and the grid's row extent is ``ceil(rows / 4)``.
+"""
+
+from __future__ import annotations
+
+from typing import Any
+
+import torch
+
+from qpu_xla_amd import _lib
+from qpu_xla_amd._tensors import ptr, require_gpu, row_stride, rows_are_dense, stream_handle
+from qpu_xla_amd.errors import KernelError
+from qpu_xla_amd.kernel import Kernel
+
+Q4_0_BLOCK_ELEMENTS = 32
+Q4_0_BLOCK_BYTES = 18
+Q8_0_BLOCK_BYTES = 34
+OUTPUT_TILE = 16
+ROW_TILE = 4
+
+
+# ----------------------------------------------------------------- block codec
+# Same byte layouts as the reference codec (ggml_q4_0.py:28-78), on torch tensors
+# of any device.
+
+
+def pack_ggml_q4_0_blocks(scales: torch.Tensor, codes: torch.Tensor) -> torch.Tensor:
+    """fp16-representable scales [...] and 0..15 codes [..., 32] -> uint8 [..., 18]."""
+    codes = torch.as_tensor(codes)
+    scales = torch.as_tensor(scales).to(torch.float16)
+    if tuple(codes.shape) != (*scales.shape, Q4_0_BLOCK_ELEMENTS) or bool(((codes < 0) | (codes > 15)).any()):
+        raise ValueError("Q4_0 codes must have scales.shape + (32,) and values in 0..15")
+    out = torch.empty((*scales.shape, Q4_0_BLOCK_BYTES), dtype=torch.uint8, device=codes.device)
+    out[..., 0:2] = scales.contiguous().view(torch.uint8).reshape(*scales.shape, 2).to(codes.device)
+    c = codes.to(torch.uint8)
+    out[..., 2:] = c[..., :16] | (c[..., 16:] << 4)
+    return out
+
+
+def pack_ggml_q8_0_blocks(scales: torch.Tensor, values: torch.Tensor) -> torch.Tensor:
+    """fp16-representable scales [...] and int8 values [..., 32] -> uint8 [..., 34]."""
+    values = torch.as_tensor(values)
+    scales = torch.as_tensor(scales).to(torch.float16)
+    if tuple(values.shape) != (*scales.shape, Q4_0_BLOCK_ELEMENTS) or bool(((values < -128) | (values > 127)).any()):
+        raise ValueError("Q8_0 values must have scales.shape + (32,) and values in -128..127")
+    out = torch.empty((*scales.shape, Q8_0_BLOCK_BYTES), dtype=torch.uint8, device=values.device)
+    out[..., 0:2] = scales.contiguous().view(torch.uint8).reshape(*scales.shape, 2).to(values.device)
+    out[..., 2:] = values.to(torch.int8).view(torch.uint8)
+    return out
+
+
+def unpack_ggml_q4_0_blocks(blocks: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """uint8 [..., 18] -> (float32 scales [...], int8 values [..., 32] in -8..7)."""
+    if blocks.dtype != torch.uint8 or blocks.dim() < 1 or blocks.shape[-1] != Q4_0_BLOCK_BYTES:
+        raise ValueError("Q4_0 blocks must be uint8 with a final extent of 18 bytes")
+    scales = blocks[..., 0:2].contiguous().view(torch.float16).squeeze(-1).to(torch.float32)
+    qs = blocks[..., 2:]
+    values = torch.cat(((qs & 0x0F).to(torch.int8) - 8, (qs >> 4).to(torch.int8) - 8), dim=-1)
+    return scales, values
+
+
+def unpack_ggml_q8_0_blocks(blocks: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """uint8 [..., 34] -> (float32 scales [...], int8 values [..., 32])."""
+    if blocks.dtype != torch.uint8 or blocks.dim() < 1 or blocks.shape[-1] != Q8_0_BLOCK_BYTES:
+        raise ValueError("Q8_0 blocks must be uint8 with a final extent of 34 bytes")
+    scales = blocks[..., 0:2].contiguous().view(torch.float16).squeeze(-1).to(torch.float32)
+    return scales, blocks[..., 2:].contiguous().view(torch.int8)
+
+
+# ------------------------------------------------------------------- operator
+
+
+def supports_ggml_q4_0_q8_0_linear(
+    activation: torch.Tensor,
+    weight: torch.Tensor,
+    destination: torch.Tensor,
+    weight_column_start: int,
+    output_column_start: int,
+    column_count: int,
+) -> bool:
+    """Whether native block tensors meet the small-M contract (ggml_q4_0.py:725-761)."""
+    tensors = (activation, weight, destination)
+    if not all(isinstance(t, torch.Tensor) for t in tensors):
+        return False
+    if any(t.device.type != "cuda" for t in tensors) or len({t.device for t in tensors}) != 1:
+        return False
+    if activation.dtype != torch.uint8 or weight.dtype != torch.uint8 or destination.dtype != torch.float32:
+        return False
+    if activation.dim() != 3 or weight.dim() != 3 or destination.dim() != 2:
+        return False
+    rows, blocks, activation_bytes = activation.shape
+    outputs, weight_blocks, weight_bytes = weight.shape
+    if rows <= 0 or activation_bytes != Q8_0_BLOCK_BYTES or weight_bytes != Q4_0_BLOCK_BYTES:
+        return False
+    if blocks <= 0 or blocks != weight_blocks or destination.shape[0] != rows:
+        return False
+    starts = (weight_column_start, output_column_start)
+    if any(s < 0 or s % OUTPUT_TILE for s in starts) or column_count <= 0 or column_count % OUTPUT_TILE:
+        return False
+    if weight_column_start + column_count > outputs or output_column_start + column_count > destination.shape[1]:
+        return False
+    return activation.is_contiguous() and weight.is_contiguous() and rows_are_dense(destination)
+
+
+def expected_grid(rows: int, column_count: int) -> tuple[int, int, int]:
+    return (column_count // OUTPUT_TILE, (rows + ROW_TILE - 1) // ROW_TILE, 1)
+
+
+def _launch_linear(activation, weight, destination, wcol0, ocol0, ncols, stream) -> None:
+    rows, blocks, _ = activation.shape
+    _lib.call(
+        "qxt_ggml_q4_0_q8_0_linear",
+        ptr(activation), row_stride(activation), ptr(weight), row_stride(weight),
+        ptr(destination), row_stride(destination),
+        rows, blocks, wcol0, ocol0, ncols, stream_handle(stream),
+    )
+
+
+def _execute_ggml_q4_0_q8_0_linear(stream: Any, args: tuple[Any, ...], grid: tuple[int, int, int]) -> None:
+    if len(args) != 6 or not all(isinstance(a, torch.Tensor) for a in args[:3]):
+        raise KernelError(
+            "GGML Q4_0 linear expects "
+            "(activation, weight, destination, weight_column_start, output_column_start, column_count)"
+        )
+    activation, weight, destination, wcol0, ocol0, ncols = args
+    if not all(isinstance(v, int) for v in (wcol0, ocol0, ncols)):
+        raise KernelError("GGML Q4_0 column bounds must be integers")
+    if not supports_ggml_q4_0_q8_0_linear(activation, weight, destination, wcol0, ocol0, ncols):
+        raise KernelError("GGML Q4_0 linear requires native contiguous Q8_0/Q4_0 blocks and aligned columns")
+    want = expected_grid(activation.shape[0], ncols)
+    if tuple(grid) != want:
+        raise KernelError(f"GGML Q4_0 linear grid must be {want}, got {tuple(grid)}")
+    _launch_linear(activation, weight, destination, wcol0, ocol0, ncols, stream)
+
+
+GGML_Q4_0_Q8_0_LINEAR_KERNEL = Kernel("gfx950.ggml_q4_0_q8_0_linear", _execute_ggml_q4_0_q8_0_linear)
+
+
+def ggml_q4_0_q8_0_linear(
+    activation: torch.Tensor,
+    weight: torch.Tensor,
+    destination: torch.Tensor | None = None,
+    *,
+    weight_column_start: int = 0,
+    output_column_start: int = 0,
+    column_count: int | None = None,
+    stream: Any = None,
+) -> torch.Tensor:
+    """Functional form: any column range (no 16-alignment), returns ``destination``."""
+    if activation.dim() != 3 or weight.dim() != 3:
+        raise ValueError("activation [M, B, 34] and weight [N, B, 18] blocks are required")
+    rows = activation.shape[0]
+    if column_count is None:
+        column_count = weight.shape[0] - weight_column_start
+    if destination is None:
+        destination = torch.empty((rows, output_column_start + column_count), dtype=torch.float32, device=weight.device)
+    require_gpu("ggml_q4_0_q8_0_linear", activation, weight, destination)
+    if not (activation.is_contiguous() and weight.is_contiguous() and rows_are_dense(destination)):
+        raise ValueError("ggml_q4_0_q8_0_linear: tensors need contiguous rows")
+    if activation.dtype != torch.uint8 or weight.dtype != torch.uint8 or destination.dtype != torch.float32:
+        raise ValueError("ggml_q4_0_q8_0_linear: uint8 blocks and a float32 destination are required")
+    if activation.shape[2] != Q8_0_BLOCK_BYTES or weight.shape[2] != Q4_0_BLOCK_BYTES or activation.shape[1] != weight.shape[1]:
+        raise ValueError("ggml_q4_0_q8_0_linear: block extents or counts do not match")
+    if weight_column_start < 0 or weight_column_start + column_count > weight.shape[0]:
+        raise ValueError("ggml_q4_0_q8_0_linear: weight column range out of bounds")
+    if output_column_start < 0 or output_column_start + column_count > destination.shape[1] or destination.shape[0] != rows:
+        raise ValueError("ggml_q4_0_q8_0_linear: destination too small")
+    _launch_linear(activation, weight, destination, weight_column_start, output_column_start, column_count, stream)
+    return destination
+
+
+def ggml_q4_0_q8_0_block_dots(
+    activation: torch.Tensor,
+    weight: torch.Tensor,
+    *,
+    weight_column_start: int = 0,
+    column_count: int | None = None,
+    stream: Any = None,
+) -> torch.Tensor:
+    """Debug path: exact int32 block dots [M, column_count, B]."""
+    rows, blocks, _ = activation.shape
+    if column_count is None:
+        column_count = weight.shape[0] - weight_column_start
+    if weight_column_start < 0 or weight_column_start + column_count > weight.shape[0]:
+        raise ValueError("block dots: weight column range out of bounds")
+    dots = torch.empty((rows, column_count, blocks), dtype=torch.int32, device=weight.device)
+    require_gpu("ggml_q4_0_q8_0_block_dots", activation, weight, dots)
+    if not (activation.is_contiguous() and weight.is_contiguous()):
+        raise ValueError("block dots: contiguous block tensors required")
+    _lib.call(
+        "qxt_ggml_q4_0_q8_0_block_dots",
+        ptr(activation), row_stride(activation), ptr(weight), row_stride(weight), ptr(dots),
+        rows, blocks, weight_column_start, column_count, stream_handle(stream),
+    )
+    return dots

@@ -1,0 +1,123 @@
+"""The C-ABI library loads, exports every declared symbol and validates on the host.
+
+No test here launches GPU work: validation and failure injection return before
+any HIP call, so these run in the GPU-less container.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from qpu_xla_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "qxt_gfx950.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(qxt_\w+)\s*\(", text, flags=re.MULTILINE)))
+
+
+def test_header_declares_the_boundary() -> None:
+    names = declared_functions()
+    for required in (
+        "qxt_quantize_q8_0",
+        "qxt_quantize_rows_int8",
+        "qxt_ggml_q4_0_q8_0_linear",
+        "qxt_w8a8_gemm_dequantize",
+        "qxt_w8a8_linear",
+    ):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol() -> None:
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} declared in the header but not exported"
+
+
+def test_binding_covers_exactly_the_header() -> None:
+    assert sorted(_lib.SIGNATURES) == declared_functions()
+
+
+def test_status_strings_and_version() -> None:
+    lib = _lib.load()
+    assert lib.qxt_abi_version() == 1
+    assert _lib.status_string(_lib.OK) == "ok"
+    assert _lib.status_string(_lib.SUBMISSION_FAILED) == "submission failed"
+    assert _lib.status_string(_lib.TIMEOUT) == "timeout"
+    assert _lib.status_string(99) == "unknown status"
+
+
+def test_failure_mask_round_trip() -> None:
+    _lib.set_failure_mask(_lib.FAIL_SUBMISSION | _lib.FAIL_WAIT)
+    try:
+        assert _lib.get_failure_mask() == _lib.FAIL_SUBMISSION | _lib.FAIL_WAIT
+    finally:
+        _lib.set_failure_mask(_lib.FAIL_NONE)
+    assert _lib.get_failure_mask() == 0
+
+
+FAKE = ctypes.c_void_p(1 << 20)  # 16-byte aligned, never dereferenced: validation or injection returns first
+
+
+@pytest.mark.parametrize(
+    "name,args,fragment",
+    [
+        ("qxt_quantize_q8_0", (None, 128, FAKE, 34, 1, 32, None), "null pointer"),
+        ("qxt_quantize_q8_0", (FAKE, 128, FAKE, 34, 1, 40, None), "multiple of 32"),
+        ("qxt_quantize_rows_int8", (FAKE, 64, FAKE, 8, FAKE, 1, 16, 8, 0, None), "padded_columns"),
+        ("qxt_quantize_rows_int8", (FAKE, 64, FAKE, 16, FAKE, 1, 16, 16, 8, None), "unknown flags"),
+        ("qxt_ggml_q4_0_q8_0_linear", (FAKE, 34, FAKE, 18, FAKE, 64, 0, 1, 0, 0, 16, None), "positive"),
+        ("qxt_ggml_q4_0_q8_0_linear", (FAKE, 33, FAKE, 18, FAKE, 64, 1, 1, 0, 0, 16, None), "strides"),
+        ("qxt_w8a8_gemm_i32", (FAKE, 16, FAKE, 16, FAKE, 64, 16, 16, 24, 0, None), "multiple of 16"),
+        ("qxt_w8a8_gemm_i32", (FAKE, 16, FAKE, 16, FAKE, 64, 16, 16, 16, 7, None), "layout"),
+        ("qxt_w8a8_gemm_i32", (FAKE, 2**20, FAKE, 2**20, FAKE, 2**20, 16, 16, 140000, 0, None), "overflow"),
+        ("qxt_w8a8_gemm_dequantize", (FAKE, 16, FAKE, 16, None, FAKE, None, FAKE, 64, 16, 16, 16, 0, None), "null"),
+        ("qxt_w8a8_dequantize", (FAKE, 64, FAKE, FAKE, None, FAKE, 32, 1, 16, None), "stride"),
+    ],
+)
+def test_invalid_arguments_are_rejected_on_the_host(name, args, fragment) -> None:
+    status = getattr(_lib.load(), name)(*args)
+    assert status == _lib.INVALID_ARGUMENT
+    assert fragment in _lib.last_error()
+
+
+def test_injected_submission_failure_returns_before_launch() -> None:
+    lib = _lib.load()
+    _lib.set_failure_mask(_lib.FAIL_SUBMISSION)
+    try:
+        status = lib.qxt_ggml_q4_0_q8_0_linear(FAKE, 34, FAKE, 18, FAKE, 64, 1, 1, 0, 0, 16, None)
+        assert status == _lib.SUBMISSION_FAILED
+        assert "injected" in _lib.last_error()
+        status = lib.qxt_w8a8_gemm_i32(FAKE, 16, FAKE, 16, FAKE, 64, 16, 16, 16, 0, None)
+        assert status == _lib.SUBMISSION_FAILED
+    finally:
+        _lib.set_failure_mask(_lib.FAIL_NONE)
+
+
+def test_injected_wait_failure_maps_to_timeout() -> None:
+    lib = _lib.load()
+    _lib.set_failure_mask(_lib.FAIL_WAIT)
+    try:
+        assert lib.qxt_stream_wait(None) == _lib.TIMEOUT
+    finally:
+        _lib.set_failure_mask(_lib.FAIL_NONE)
+
+
+def test_qxt_error_carries_status_and_message() -> None:
+    with pytest.raises(_lib.QxtError) as info:
+        _lib.call("qxt_quantize_q8_0", None, 128, FAKE, 34, 1, 32, None)
+    assert info.value.status == _lib.INVALID_ARGUMENT
+    assert "null pointer" in str(info.value)
+
+
+def test_q4_0_linear_rejects_k_beyond_the_lds_budget_before_launch() -> None:
+    # K = 131072 needs more than 64 KB of LDS for the staged activation row.
+    status = _lib.load().qxt_ggml_q4_0_q8_0_linear(FAKE, 4096 * 34, FAKE, 4096 * 18, FAKE, 64, 1, 4096, 0, 0, 16, None)
+    assert status == _lib.CAPABILITY_MISSING
+    assert "LDS" in _lib.last_error()

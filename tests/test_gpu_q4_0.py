@@ -1,0 +1,167 @@
+"""GPU parity of the Q4_0 x Q8_0 linear against the NumPy oracle (bit-exact)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import load_golden
+from qpu_xla_amd import KernelError, Queue, _lib
+from qpu_xla_amd.kernels import ggml_q4_0 as q4
+
+pytestmark = pytest.mark.gpu
+
+SENTINEL = np.float32(123456.0)
+
+
+def dev(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+
+
+def random_blocks(rng, rows, blocks, outputs):
+    act = oracle.pack_q8_0_blocks(
+        rng.uniform(0.0001, 0.2, (rows, blocks)).astype(np.float16), rng.integers(-128, 128, (rows, blocks, 32))
+    )
+    wt = oracle.pack_q4_0_blocks(
+        rng.uniform(-0.2, 0.2, (outputs, blocks)).astype(np.float16), rng.integers(0, 16, (outputs, blocks, 32))
+    )
+    return act, wt
+
+
+@pytest.mark.parametrize("name", ["kat_q4_0_m1", "kat_q4_0_m4", "kat_q4_0_mx"])
+def test_native_smoke_kats_through_the_queue_contract(name: str) -> None:
+    # Resident partition [16, 32) as in qpu_llama_q4_0_smoke.c; columns 0..15 keep the sentinel.
+    g = load_golden(name)
+    rows = g["activation"].shape[0]
+    start = int(g["resident_start"])
+    resident = dev(g["weight"][start:])
+    destination = torch.full((rows, g["weight"].shape[0]), float(SENTINEL), device="cuda")
+    with Queue() as queue:
+        queue.submit(
+            q4.GGML_Q4_0_Q8_0_LINEAR_KERNEL,
+            (dev(g["activation"]), resident, destination, 0, start, int(g["resident_count"])),
+            grid=q4.expected_grid(rows, int(g["resident_count"])),
+        ).wait()
+    out = destination.cpu().numpy()
+    np.testing.assert_array_equal(out[:, :start], SENTINEL)
+    np.testing.assert_array_equal(out[:, start:], g["expected"][:, start:])
+
+
+def test_reference_seed_fixture_bit_exact_and_block_dots() -> None:
+    # Inputs of tests/test_qpu_xla_ggml_q4_0.py:47-80 (seed 4404).
+    g = load_golden("oracle_q4_0_linear_seed4404")
+    act, wt = dev(g["activation"]), dev(g["weight"])
+    out = q4.ggml_q4_0_q8_0_linear(act, wt)
+    np.testing.assert_array_equal(out.cpu().numpy(), g["expected"])
+    dots = q4.ggml_q4_0_q8_0_block_dots(act, wt)
+    np.testing.assert_array_equal(dots.cpu().numpy(), g["dots"])
+
+
+@pytest.mark.parametrize(
+    "rows,blocks,outputs",
+    [
+        (1, 1, 16),      # generic path, single block
+        (1, 3, 50),      # generic path, ragged N
+        (2, 8, 33),      # fast path, ragged N
+        (3, 16, 64),
+        (4, 64, 5632),   # cfg0-like K=2048 at M=4
+        (1, 176, 100),   # K=5632 (22 units of 8 blocks)
+        (5, 24, 40),     # row group 4 + 1
+        (16, 8, 48),
+        (1, 1024, 16),   # K=32768: 128 units per column, two columns per workgroup
+    ],
+)
+def test_random_shapes_bit_exact(rows: int, blocks: int, outputs: int) -> None:
+    rng = np.random.default_rng(rows * 1000 + blocks * 10 + outputs)
+    act, wt = random_blocks(rng, rows, blocks, outputs)
+    out = q4.ggml_q4_0_q8_0_linear(dev(act), dev(wt))
+    np.testing.assert_array_equal(out.cpu().numpy(), oracle.q4_0_q8_0_reference(act, wt))
+    dots = q4.ggml_q4_0_q8_0_block_dots(dev(act), dev(wt))
+    np.testing.assert_array_equal(dots.cpu().numpy(), oracle.q4_0_q8_0_block_dots(act, wt))
+
+
+def test_every_aligned_subrange_of_48_columns_leaves_the_rest_untouched() -> None:
+    # qpu_llama_native_safety_smoke.c: every aligned 16-column subrange of 48 columns.
+    rng = np.random.default_rng(48)
+    act, wt = random_blocks(rng, 4, 8, 48)
+    expected = oracle.q4_0_q8_0_reference(act, wt)
+    a, w = dev(act), dev(wt)
+    for start in range(0, 48, 16):
+        for count in range(16, 48 - start + 1, 16):
+            destination = torch.full((4, 48), float(SENTINEL), device="cuda")
+            q4.ggml_q4_0_q8_0_linear(a, w, destination, weight_column_start=start,
+                                     output_column_start=start, column_count=count)
+            out = destination.cpu().numpy()
+            np.testing.assert_array_equal(out[:, start:start + count], expected[:, start:start + count])
+            mask = np.ones(48, bool)
+            mask[start:start + count] = False
+            np.testing.assert_array_equal(out[:, mask], SENTINEL)
+
+
+def test_sequential_block_order_is_reproduced() -> None:
+    # ((0 + 1) + 2**-24) - 1 == 0 only when blocks are summed in order.
+    codes = np.full((1, 3, 32), 8, np.uint8)
+    codes[0, :, 0] = 9
+    a_vals = np.zeros((1, 3, 32), np.int16)
+    a_vals[0, :, 0] = [1, 1, -1]
+    act = oracle.pack_q8_0_blocks(np.array([[1.0, 2.0**-12, 1.0]], np.float16), a_vals)
+    wt = oracle.pack_q4_0_blocks(np.array([[1.0, 2.0**-12, 1.0]], np.float16), codes)
+    wt16 = np.repeat(wt, 16, axis=0)
+    out = q4.ggml_q4_0_q8_0_linear(dev(act), dev(wt16)).cpu().numpy()
+    np.testing.assert_array_equal(out, np.zeros((1, 16), np.float32))
+
+
+def test_contract_errors_leave_destination_untouched() -> None:
+    rng = np.random.default_rng(5)
+    act, wt = random_blocks(rng, 4, 8, 32)
+    a, w = dev(act), dev(wt)
+    destination = torch.full((4, 32), float(SENTINEL), device="cuda")
+    with Queue() as queue:
+        with pytest.raises(KernelError, match="grid"):
+            queue.submit(q4.GGML_Q4_0_Q8_0_LINEAR_KERNEL, (a, w, destination, 0, 0, 32), grid=(1, 1, 1))
+        with pytest.raises(KernelError, match="aligned"):
+            queue.submit(q4.GGML_Q4_0_Q8_0_LINEAR_KERNEL, (a, w, destination, 8, 0, 16), grid=(1, 1, 1))
+        _lib.set_failure_mask(_lib.FAIL_SUBMISSION)
+        try:
+            with pytest.raises(KernelError):
+                queue.submit(q4.GGML_Q4_0_Q8_0_LINEAR_KERNEL, (a, w, destination, 0, 0, 32), grid=(2, 1, 1))
+        finally:
+            _lib.set_failure_mask(_lib.FAIL_NONE)
+        queue.synchronize()
+    np.testing.assert_array_equal(destination.cpu().numpy(), SENTINEL)
+
+
+def _cfg_case(seed: int, rows: int, k: int, n: int):
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    x = rng.standard_normal((rows, k), dtype=np.float32)
+    return w, x
+
+
+@pytest.mark.parametrize(
+    "seed,rows,k,n",
+    [
+        (0, 1, 2048, 5632),   # BASELINE cfg0: TinyLlama FFN-up, M=1
+        (2, 4, 4096, 4096),   # cfg2 (second shape), M=4
+        (2, 4, 4096, 11008),  # cfg2 (first shape), M=4
+        (3, 1, 5632, 2048),   # cfg3 down projection
+        (3, 1, 2048, 256),    # cfg3 k/v projection
+    ],
+)
+def test_baseline_configs_end_to_end_bit_exact(seed: int, rows: int, k: int, n: int) -> None:
+    from qpu_xla_amd.kernels.quantize import quantize_q4_0, quantize_q8_0
+
+    w, x = _cfg_case(seed, rows, k, n)
+    wq = quantize_q4_0(dev(w))
+    xq = quantize_q8_0(dev(x))
+    wq_ref = oracle.quantize_q4_0_blocks(w)
+    xq_ref = oracle.quantize_q8_0_blocks(x)
+    np.testing.assert_array_equal(wq.cpu().numpy(), wq_ref)
+    np.testing.assert_array_equal(xq.cpu().numpy(), xq_ref)
+    out = q4.ggml_q4_0_q8_0_linear(xq, wq).cpu().numpy()
+    expected = oracle.q4_0_q8_0_reference(xq_ref, wq_ref)
+    np.testing.assert_array_equal(out, expected)
+    # The north-star tolerance (rel 1e-5 of max|ref|) holds a fortiori.
+    assert np.abs(out - expected).max() <= 1e-5 * np.abs(expected).max()

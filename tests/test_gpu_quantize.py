@@ -1,0 +1,87 @@
+"""GPU parity of the Q8_0, per-row int8 and Q4_0 quantisers (bit-exact codes and scales)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import load_golden
+from qpu_xla_amd.kernels.quantize import quantize_q4_0, quantize_q8_0, quantize_rows_int8
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+
+
+def test_fixture_vectors() -> None:
+    g = load_golden("oracle_quantizers_seed2024")
+    x = dev(g["x"])
+    np.testing.assert_array_equal(quantize_q8_0(x).cpu().numpy(), g["q8_0_blocks"])
+    q, s = quantize_rows_int8(x)
+    np.testing.assert_array_equal(q.cpu().numpy(), g["rows_q"])
+    np.testing.assert_array_equal(s.cpu().numpy(), g["rows_scale"])
+    np.testing.assert_array_equal(quantize_q4_0(dev(g["w"])).cpu().numpy(), g["q4_0_blocks"])
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 32), (3, 96), (7, 2048), (64, 5632), (2, 14336)])
+def test_q8_0_random_bit_exact(rows: int, cols: int) -> None:
+    rng = np.random.default_rng(rows + cols)
+    x = rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(rng.uniform(0.01, 10))
+    x[0, :32] = 0.0
+    np.testing.assert_array_equal(quantize_q8_0(dev(x)).cpu().numpy(), oracle.quantize_q8_0_blocks(x))
+
+
+def test_q8_0_half_even_ties_and_tiny_scales() -> None:
+    x = np.zeros((2, 64), np.float32)
+    x[0, :6] = [127.0, 2.5, 3.5, -2.5, -3.5, 0.5]
+    x[1, :32] = np.float32(1e-6) * np.arange(32, dtype=np.float32)  # subnormal fp16 scale
+    x[1, 32:] = np.float32(7e4) * np.sin(np.arange(32, dtype=np.float32))  # scale near fp16 max
+    np.testing.assert_array_equal(quantize_q8_0(dev(x)).cpu().numpy(), oracle.quantize_q8_0_blocks(x))
+
+
+@pytest.mark.parametrize("rows,cols,pad", [(1, 16, 16), (5, 300, 304), (8, 4096, 4096), (3, 14336, 14336), (2, 20000, 20000), (4, 5, 16)])
+def test_rows_int8_random_bit_exact(rows: int, cols: int, pad: int) -> None:
+    rng = np.random.default_rng(cols)
+    x = rng.standard_normal((rows, cols), dtype=np.float32)
+    x[-1] *= np.float32(1e-3)  # floor active on the last row
+    q, s = quantize_rows_int8(dev(x), padded_columns=pad)
+    qr, sr = oracle.quantize_rows_int8(x)
+    np.testing.assert_array_equal(s.cpu().numpy(), sr)
+    qn = q.cpu().numpy()
+    np.testing.assert_array_equal(qn[:, :cols], qr)
+    np.testing.assert_array_equal(qn[:, cols:], 0)
+
+
+def test_rows_int8_outlier_channels_like_cfg4() -> None:
+    rng = np.random.default_rng(4)
+    k = 4096
+    x = rng.standard_normal((64, k), dtype=np.float32)
+    outliers = rng.choice(k, round(0.001 * k), replace=False)
+    x[:, outliers] *= np.float32(20.0)
+    q, s = quantize_rows_int8(dev(x))
+    qr, sr = oracle.quantize_rows_int8(x)
+    np.testing.assert_array_equal(q.cpu().numpy(), qr)
+    np.testing.assert_array_equal(s.cpu().numpy(), sr)
+
+
+def test_rows_int8_without_floor_is_labelled_non_reference() -> None:
+    x = np.zeros((2, 32), np.float32)
+    x[1] = np.float32(1e-4) * np.arange(32, dtype=np.float32)
+    q, s = quantize_rows_int8(dev(x), floor=False)
+    qr, sr = oracle.quantize_rows_int8(x, floor=False)
+    np.testing.assert_array_equal(s.cpu().numpy(), sr)
+    np.testing.assert_array_equal(q.cpu().numpy(), qr)
+
+
+@pytest.mark.parametrize("rows,cols", [(4, 32), (9, 256), (256, 2048), (16, 5632)])
+def test_q4_0_weights_bit_exact(rows: int, cols: int) -> None:
+    rng = np.random.default_rng(rows * cols)
+    w = rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.02)
+    w[0, :32] = 0.0
+    w[1, :32] = np.float32(0.5)  # ties in |max|: first element wins
+    w[1, 5] = np.float32(-0.5)
+    np.testing.assert_array_equal(quantize_q4_0(dev(w)).cpu().numpy(), oracle.quantize_q4_0_blocks(w))

@@ -1,0 +1,166 @@
+"""GPU parity of the W8A8 int8 MFMA GEMM, its epilogue and the whole linear (bit-exact)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import load_golden
+from qpu_xla_amd import DependencyError, Queue
+from qpu_xla_amd.kernels import gemm_int8, gemv_int8, w8a8_epilogue
+from qpu_xla_amd.quantization import PreparedW8A8Linear, QuantizedMatrixInt8, quantize_per_output_channel_int8, w8a8_linear
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+
+
+def words(a: np.ndarray) -> torch.Tensor:
+    return dev(np.ascontiguousarray(a).view(np.int32))
+
+
+def test_native_w8a8_smoke_kat_through_gemv_kernel() -> None:
+    g = load_golden("kat_w8a8")
+    left, right = oracle.pack_int8_gemm_operands(g["activation"], g["weight_kn"])
+    destination = torch.full((1, 16), -1, dtype=torch.int32, device="cuda")
+    with Queue() as queue:
+        queue.submit(gemv_int8.W8A8_GEMV_KERNEL, (words(left), words(right), destination), grid=(1, 1, 1)).wait()
+    np.testing.assert_array_equal(destination.cpu().numpy(), g["expected"])
+
+
+@pytest.mark.parametrize("shape", [(16, 16, 16), (32, 64, 32)])
+def test_tiled_gemm_packed_operands_exact(shape) -> None:
+    # tests/test_qpu_xla_gemm_int8.py:28-54 (seed 91 + q).
+    p, q, r = shape
+    rng = np.random.default_rng(91 + q)
+    left_v = rng.integers(-127, 128, size=(p, q), dtype=np.int8)
+    right_v = rng.integers(-127, 128, size=(q, r), dtype=np.int8)
+    left, right = oracle.pack_int8_gemm_operands(left_v, right_v)
+    destination = torch.empty((p, r), dtype=torch.int32, device="cuda")
+    with Queue() as queue:
+        queue.submit(gemm_int8.TILED_W8A8_GEMM_KERNEL, (words(left), words(right), destination),
+                     grid=(r // 16, p // 16, 1)).wait()
+    expected = (left_v.astype(np.int64) @ right_v.astype(np.int64)).astype(np.int32)
+    np.testing.assert_array_equal(destination.cpu().numpy(), expected)
+
+
+def test_fused_dequantize_fixture_bit_exact() -> None:
+    # tests/test_qpu_xla_gemm_int8.py:57-92 (seed 1765), assert_array_equal as the reference does.
+    g = load_golden("oracle_w8a8_fused_seed1765")
+    left, right = oracle.pack_int8_gemm_operands(g["left"], g["right"])
+    p, r = g["expected"].shape
+    destination = torch.empty((p, r), dtype=torch.float32, device="cuda")
+    with Queue() as queue:
+        queue.submit(
+            gemm_int8.TILED_W8A8_GEMM_DEQUANTIZE_KERNEL,
+            (words(left), words(right), dev(g["row_scales"]), dev(g["column_scales"]), destination),
+            grid=(r // 16, p // 16, 1),
+        ).wait()
+    np.testing.assert_array_equal(destination.cpu().numpy(), g["expected"])
+    # Same through the natural [N, K] weight layout.
+    out = gemm_int8.w8a8_gemm_dequantize(dev(g["left"]), dev(np.ascontiguousarray(g["right"].T)),
+                                         dev(g["row_scales"]), dev(g["column_scales"]))
+    np.testing.assert_array_equal(out.cpu().numpy(), g["expected"])
+
+
+@pytest.mark.parametrize(
+    "m,n,k",
+    [(1, 16, 16), (7, 33, 48), (129, 257, 64), (128, 128, 4096), (300, 1000, 1040), (1, 4096, 14336), (64, 14336, 4096)],
+)
+def test_gemm_i32_random_shapes_exact(m: int, n: int, k: int) -> None:
+    rng = np.random.default_rng(m * 7 + n * 3 + k)
+    a = rng.integers(-127, 128, size=(m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    out = gemm_int8.w8a8_gemm_i32(dev(a), dev(w))
+    np.testing.assert_array_equal(out.cpu().numpy(), oracle.int8_gemm_i32(a, w))
+
+
+def test_gemm_i32_extreme_accumulators_exact() -> None:
+    k = 4096
+    a = np.full((32, k), 127, np.int8)
+    a[1::2] = -127
+    w = np.full((32, k), 127, np.int8)
+    out = gemm_int8.w8a8_gemm_i32(dev(a), dev(w)).cpu().numpy()
+    assert out[0, 0] == k * 127 * 127 and out[1, 0] == -k * 127 * 127
+    np.testing.assert_array_equal(out, oracle.int8_gemm_i32(a, w))
+
+
+def test_epilogue_rounds_each_step_and_adds_bias_separately() -> None:
+    s = np.full(16, 1 + 2.0**-12, np.float32)
+    a = np.zeros((16, 16), np.int8)
+    a[:, 0] = 1
+    w = np.zeros((16, 16), np.int8)
+    w[:, 0] = 1
+    bias = np.full(16, -1.0, np.float32)
+    out = gemm_int8.w8a8_gemm_dequantize(dev(a), dev(w), dev(s), dev(s), dev(bias)).cpu().numpy()
+    np.testing.assert_array_equal(out, np.full((16, 16), 2.0**-11, np.float32))
+    acc = torch.ones((16, 16), dtype=torch.int32, device="cuda")
+    out2 = w8a8_epilogue.w8a8_dequantize(acc, dev(s), dev(s), dev(bias)).cpu().numpy()
+    np.testing.assert_array_equal(out2, out)
+
+
+def test_standalone_dequantize_kernel_contract() -> None:
+    rng = np.random.default_rng(9)
+    acc = rng.integers(-2**24, 2**24, size=(32, 48), dtype=np.int32)
+    sa = rng.uniform(0.001, 0.1, 32).astype(np.float32)
+    sw = rng.uniform(0.001, 0.1, 48).astype(np.float32)
+    destination = torch.empty((32, 48), dtype=torch.float32, device="cuda")
+    with Queue() as queue:
+        queue.submit(w8a8_epilogue.W8A8_DEQUANTIZE_KERNEL, (dev(acc), dev(sa), dev(sw), destination),
+                     grid=(3, 2, 1)).wait()
+    np.testing.assert_array_equal(destination.cpu().numpy(), oracle.dequantize_epilogue(acc, sa, sw))
+
+
+@pytest.mark.parametrize("m,k,n,seed", [(512, 512, 512, 1), (1, 512, 512, 1731), (37, 2048, 5632, 5)])
+def test_whole_linear_bit_exact(m: int, k: int, n: int, seed: int) -> None:
+    # cfg1 (M=K=N=512; x ~ N(0,1), W ~ N(0,0.05): weight floor active, bias ~ N(0,0.1)).
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.05)).astype(np.float32)
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    bias = (rng.standard_normal(n, dtype=np.float32) * np.float32(0.1)).astype(np.float32)
+    weight = quantize_per_output_channel_int8(dev(w))
+    qw, sw = oracle.quantize_per_output_channel_int8(w)
+    np.testing.assert_array_equal(weight.values.cpu().numpy(), qw)
+    np.testing.assert_array_equal(weight.scales.cpu().numpy(), sw)
+    y = w8a8_linear(dev(x), weight, dev(bias)).cpu().numpy()
+    np.testing.assert_array_equal(y, oracle.w8a8_linear_reference(x, qw, sw, bias))
+
+
+def test_cfg4_shape_sampled_rows_bit_exact() -> None:
+    # cfg4 (M=4096, K=4096, N=14336, 0.1% outlier channels x20): all rows on the GPU,
+    # the oracle on 48 sampled rows (the oracle's cost, not the kernel's, sets the sample).
+    rng = np.random.default_rng(4)
+    m, k, n = 4096, 4096, 14336
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    x[:, rng.choice(k, round(0.001 * k), replace=False)] *= np.float32(20.0)
+    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    bias = (rng.standard_normal(n, dtype=np.float32) * np.float32(0.1)).astype(np.float32)
+    weight = quantize_per_output_channel_int8(dev(w))
+    y = w8a8_linear(dev(x), weight, dev(bias))
+    rows = np.sort(rng.choice(m, 48, replace=False))
+    rows[0], rows[-1] = 0, m - 1
+    qw, sw = oracle.quantize_per_output_channel_int8(w)
+    expected = oracle.w8a8_linear_reference(x[rows], qw, sw, bias)
+    np.testing.assert_array_equal(y[torch.from_numpy(rows).cuda()].cpu().numpy(), expected)
+
+
+def test_prepared_plan_binds_queue_pads_k_and_matches_oracle() -> None:
+    rng = np.random.default_rng(77)
+    k, n = 100, 48  # K not a multiple of 16: the plan pads with zero columns
+    w = rng.standard_normal((n, k), dtype=np.float32)
+    x = rng.standard_normal((5, k), dtype=np.float32)
+    bias = rng.standard_normal(n, dtype=np.float32)
+    qw, sw = oracle.quantize_per_output_channel_int8(w)
+    weight = QuantizedMatrixInt8(dev(qw), dev(sw))
+    destination = torch.empty((5, n), dtype=torch.float32, device="cuda")
+    with Queue() as queue, Queue() as other, PreparedW8A8Linear(weight, max_batch=8, bias=dev(bias)) as plan:
+        plan.execute(destination, dev(x), queue=queue).wait()
+        np.testing.assert_array_equal(destination.cpu().numpy(), oracle.w8a8_linear_reference(x, qw, sw, bias))
+        with pytest.raises(DependencyError):
+            plan.execute(destination, dev(x), queue=other)
+        with pytest.raises(ValueError):
+            plan.execute(torch.empty((9, n), device="cuda"), dev(np.zeros((9, k), np.float32)), queue=queue)

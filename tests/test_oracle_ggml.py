@@ -1,0 +1,171 @@
+"""Pin the NumPy oracle of the GGML path against closed forms, KATs and brute force."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import load_golden
+
+
+def test_codec_extremes_match_reference_cases() -> None:
+    # tests/test_qpu_xla_ggml_q4_0.py:25-44 in the reference.
+    g = load_golden("codec_extremes")
+    blocks = oracle.pack_q4_0_blocks(g["q4_scales"], g["q4_codes"])
+    scales, values = oracle.unpack_q4_0_blocks(blocks)
+    np.testing.assert_array_equal(scales, g["q4_scales"].astype(np.float32))
+    np.testing.assert_array_equal(values, g["q4_codes"].astype(np.int8) - 8)
+    q8 = oracle.pack_q8_0_blocks(g["q8_scales"], g["q8_values"])
+    s8, v8 = oracle.unpack_q8_0_blocks(q8)
+    np.testing.assert_array_equal(s8, g["q8_scales"].astype(np.float32))
+    np.testing.assert_array_equal(v8, g["q8_values"].astype(np.int8))
+
+
+def test_q4_0_byte_layout_low_nibble_is_element_j_high_is_j_plus_16() -> None:
+    codes = np.arange(32, dtype=np.uint8) % 16
+    codes[16:] = 15 - codes[16:]
+    block = oracle.pack_q4_0_blocks(np.array([1.0], np.float16), codes[None])[0]
+    assert block[0] == 0x00 and block[1] == 0x3C  # little-endian fp16 1.0
+    for j in range(16):
+        assert block[2 + j] & 0x0F == codes[j]
+        assert block[2 + j] >> 4 == codes[16 + j]
+
+
+def test_codec_round_trip_random() -> None:
+    rng = np.random.default_rng(7)
+    scales = rng.uniform(-2, 2, size=(5, 7)).astype(np.float16)
+    codes = rng.integers(0, 16, size=(5, 7, 32), dtype=np.uint8)
+    s, v = oracle.unpack_q4_0_blocks(oracle.pack_q4_0_blocks(scales, codes))
+    np.testing.assert_array_equal(s, scales.astype(np.float32))
+    np.testing.assert_array_equal(v.astype(np.int16) + 8, codes)
+    values = rng.integers(-128, 128, size=(3, 4, 32), dtype=np.int16)
+    s8, v8 = oracle.unpack_q8_0_blocks(oracle.pack_q8_0_blocks(scales[:3, :4], values))
+    np.testing.assert_array_equal(v8, values.astype(np.int8))
+
+
+@pytest.mark.parametrize("name", ["kat_q4_0_m1", "kat_q4_0_m4", "kat_q4_0_mx"])
+def test_q4_0_reference_matches_native_smoke_kats(name: str) -> None:
+    g = load_golden(name)
+    actual = oracle.q4_0_q8_0_reference(g["activation"], g["weight"])
+    np.testing.assert_array_equal(actual, g["expected"])
+
+
+def test_q4_0_block_dots_match_dequantised_brute_force() -> None:
+    rng = np.random.default_rng(11)
+    rows, blocks, outputs = 3, 4, 5
+    act = oracle.pack_q8_0_blocks(
+        rng.uniform(-0.1, 0.1, (rows, blocks)).astype(np.float16), rng.integers(-128, 128, (rows, blocks, 32))
+    )
+    wt = oracle.pack_q4_0_blocks(
+        rng.uniform(-0.2, 0.2, (outputs, blocks)).astype(np.float16), rng.integers(0, 16, (outputs, blocks, 32))
+    )
+    dots = oracle.q4_0_q8_0_block_dots(act, wt)
+    for m in range(rows):
+        for n in range(outputs):
+            for b in range(blocks):
+                a = [int(np.int8(x)) for x in act[m, b, 2:].view(np.int8)]
+                w = [(int(wt[n, b, 2 + j]) & 15) - 8 for j in range(16)] + [(int(wt[n, b, 2 + j]) >> 4) - 8 for j in range(16)]
+                assert dots[m, n, b] == sum(x * y for x, y in zip(a, w))
+
+
+def test_q4_0_reference_matches_float64_dequantised_sum() -> None:
+    rng = np.random.default_rng(4850)
+    rows, blocks, outputs = 4, 9, 7
+    act = oracle.pack_q8_0_blocks(
+        rng.uniform(-0.1, 0.1, (rows, blocks)).astype(np.float16), rng.integers(-128, 128, (rows, blocks, 32))
+    )
+    wt = oracle.pack_q4_0_blocks(
+        rng.uniform(-0.2, 0.2, (outputs, blocks)).astype(np.float16), rng.integers(0, 16, (outputs, blocks, 32))
+    )
+    sa, va = oracle.unpack_q8_0_blocks(act)
+    sw, vw = oracle.unpack_q4_0_blocks(wt)
+    a = sa.astype(np.float64)[..., None] * va.astype(np.float64)
+    w = sw.astype(np.float64)[..., None] * vw.astype(np.float64)
+    expected = np.einsum("rbk,obk->ro", a, w)
+    actual = oracle.q4_0_q8_0_reference(act, wt)
+    np.testing.assert_allclose(actual, expected, rtol=2e-5, atol=2e-5 * np.abs(expected).max())
+
+
+def test_q4_0_reference_power_of_two_scales_are_exact() -> None:
+    rng = np.random.default_rng(3)
+    rows, blocks, outputs = 2, 6, 9
+    a_scales = (2.0 ** rng.integers(-6, 2, (rows, blocks))).astype(np.float16)
+    w_scales = (2.0 ** rng.integers(-6, 2, (outputs, blocks)) * rng.choice([-1, 1], (outputs, blocks))).astype(np.float16)
+    act = oracle.pack_q8_0_blocks(a_scales, rng.integers(-128, 128, (rows, blocks, 32)))
+    wt = oracle.pack_q4_0_blocks(w_scales, rng.integers(0, 16, (outputs, blocks, 32)))
+    dots = oracle.q4_0_q8_0_block_dots(act, wt).astype(np.float64)
+    expected = np.einsum("mnb,nb,mb->mn", dots, w_scales.astype(np.float64), a_scales.astype(np.float64))
+    np.testing.assert_array_equal(oracle.q4_0_q8_0_reference(act, wt), expected.astype(np.float32))
+
+
+def test_q4_0_reference_sums_blocks_sequentially() -> None:
+    # c_0 = 1, c_1 = 2**-24, c_2 = -1: ((0 + 1) + 2**-24) - 1 == 0 in fp32 (the
+    # middle add ties to even), while any other association gives 2**-24.
+    act = np.zeros((1, 3, 34), np.uint8)
+    wt = np.zeros((1, 3, 18), np.uint8)
+    codes = np.full((1, 3, 32), 8, np.uint8)
+    codes[0, :, 0] = 9  # element 0 contributes +1 per unit activation
+    a_vals = np.zeros((1, 3, 32), np.int16)
+    a_vals[0, :, 0] = [1, 1, -1]
+    act[:] = oracle.pack_q8_0_blocks(np.array([[1.0, 2.0**-12, 1.0]], np.float16), a_vals)
+    wt[:] = oracle.pack_q4_0_blocks(np.array([[1.0, 2.0**-12, 1.0]], np.float16), codes)
+    assert oracle.q4_0_q8_0_reference(act, wt)[0, 0] == np.float32(0.0)
+
+
+def test_q8_0_quantiser_invariants() -> None:
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((6, 512), dtype=np.float32) * np.float32(3.0)
+    x[2, 64:96] = 0.0
+    scale_bits, codes = oracle.quantize_q8_0_split(x)
+    g = x.reshape(6, 16, 32)
+    q = codes.reshape(6, 16, 32).astype(np.int32)
+    d16 = scale_bits.view(np.float16)
+    amax = np.abs(g).max(axis=2)
+    d32 = amax / np.float32(127.0)
+    np.testing.assert_array_equal(d16, d32.astype(np.float16))  # fp16 RNE storage
+    assert np.all(np.abs(q) <= 127)
+    nz = amax > 0
+    hit = np.take_along_axis(q, np.abs(g).argmax(axis=2)[..., None], axis=2)[..., 0]
+    assert np.all(np.abs(hit[nz]) == 127)
+    np.testing.assert_array_equal(q[~nz], 0)
+    err = np.abs(g - q * d32[..., None])
+    assert np.all(err <= d32[..., None] * 0.5000001 + 1e-12)
+
+
+def test_q8_0_quantiser_rounds_half_to_even() -> None:
+    x = np.zeros((1, 32), np.float32)
+    x[0, :6] = [127.0, 2.5, 3.5, -2.5, -3.5, 0.5]  # absmax 127 -> d = 1, inv = 1
+    _, codes = oracle.quantize_q8_0_split(x)
+    np.testing.assert_array_equal(codes[0, :6], [127, 2, 4, -2, -4, 0])
+
+
+def test_q8_0_blocks_equal_split_form() -> None:
+    g = load_golden("oracle_quantizers_seed2024")
+    bits, codes = oracle.quantize_q8_0_split(g["x"])
+    blocks = g["q8_0_blocks"]
+    np.testing.assert_array_equal(blocks[..., 0:2].copy().view("<u2")[..., 0], bits)
+    np.testing.assert_array_equal(blocks[..., 2:].reshape(codes.shape).view(np.int8), codes)
+
+
+def test_q4_0_quantiser_invariants_parity_unpinned_vs_ggml() -> None:
+    # Only the BASELINE formula's invariants are checked (ggml is not vendored).
+    rng = np.random.default_rng(9)
+    w = rng.standard_normal((8, 256), dtype=np.float32) * np.float32(0.02)
+    w[3, :32] = 0.0
+    blocks = oracle.quantize_q4_0_blocks(w)
+    d, v = oracle.unpack_q4_0_blocks(blocks)
+    g = w.reshape(8, 8, 32)
+    first = np.abs(g).argmax(axis=2)
+    signed_max = np.take_along_axis(g, first[..., None], axis=2)[..., 0]
+    np.testing.assert_array_equal(d, (signed_max / np.float32(-8)).astype(np.float16).astype(np.float32))
+    codes = v.astype(np.int32) + 8
+    assert codes.min() >= 0 and codes.max() <= 15
+    nz = np.abs(signed_max) > 0
+    np.testing.assert_array_equal(np.take_along_axis(codes, first[..., None], axis=2)[..., 0][nz], 0)
+    dq = v.astype(np.float32) * d[..., None]
+    step = np.abs(d)[..., None]
+    assert np.all(np.abs(dq - g) <= step * 1.01 + 1e-9)
+    # All-zero block: d = -0.0 (fp16 0x8000) and every code 8, as ggml's rule gives.
+    assert blocks[3, 0, 0] == 0x00 and blocks[3, 0, 1] == 0x80
+    np.testing.assert_array_equal(codes[3, 0], 8)
