@@ -5,10 +5,12 @@ Headline (``value``): Q4_0 x Q8_0 M=1 throughput in GB/s on BASELINE cfg3, the
 TinyLlama-1.1B-shaped decode step -- 22 layers x 7 linears (q, k, v, o, gate,
 up, down), each activation re-quantised to Q8_0 right before its GEMV, 545 MB
 of Q4_0 weights per step (beyond the 256 MB MALL, so every step streams HBM).
-A step is the 308 kernels (154 quantise + 154 GEMV) replayed as one HIP graph.
+A step is all 154 quantise+GEMV tasks in one batched launch (the cfg3 linears
+read independent activations); the dependency-staged schedule (88 launches per
+step) and one-kernel-per-linear schedule (308 launches) are reported beside it.
 
 Also reported on the same JSON line:
-  * ``roofline``      -- the Q4_0 linear kernel's achieved HBM GB/s from its own
+  * ``roofline``      -- the batched Q4_0 kernel's achieved HBM GB/s from its own
                           per-launch device time (hipExtLaunchKernel events);
   * ``w8a8``          -- cfg4 dynamic-W8A8 prefill GEMMs (M=4096) in TOPS, whole
                           operator and GEMM-only, with an int8-MFMA roofline;
@@ -141,57 +143,134 @@ def _rs(t) -> int:
 # --------------------------------------------------------------------- legs
 
 
-def leg_decode(torch, args) -> dict:
-    """cfg3: 22 x 7 Q4_0 linears at M=1, each preceded by its Q8_0 quantisation."""
+def _decode_model(torch, gen):
+    """cfg3 tensors: per linear (k, n, Q4_0 weight, fp32 activation, Q8_0 buffer, output)."""
     from qpu_xla_amd.kernels.quantize import quantize_q4_0
 
-    gen = torch.Generator(device="cuda")
-    gen.manual_seed(3)
-    stream = torch.cuda.Stream()
-    runner = Runner(torch, stream)
-    keep = []
-    bytes_step = 0
-    q4_bytes_launches = []
+    model = []
     for _layer in range(LAYERS):
-        for _name, k, n in TINYLLAMA_LAYER:
+        layer = []
+        for name, k, n in TINYLLAMA_LAYER:
             w = torch.randn((n, k), generator=gen, device="cuda", dtype=torch.float32) * 0.02
             wq = quantize_q4_0(w)
             del w
             x = torch.randn((1, k), generator=gen, device="cuda", dtype=torch.float32)
             xq = torch.empty((1, k // 32, 34), dtype=torch.uint8, device="cuda")
             y = torch.empty((1, n), dtype=torch.float32, device="cuda")
-            keep.append((wq, x, xq, y))
-            runner.add("qxt_quantize_q8_0", _p(x), _rs(x), _p(xq), _rs(xq), 1, k, runner.handle)
-            runner.add("qxt_ggml_q4_0_q8_0_linear", _p(xq), _rs(xq), _p(wq), _rs(wq), _p(y), _rs(y),
-                       1, k // 32, 0, 0, n, runner.handle)
-            b = q4_linear_bytes(1, k, n)
-            bytes_step += b
-            q4_bytes_launches.append(b)
+            layer.append({"name": name, "k": k, "n": n, "weight": wq, "x": x, "xq": xq, "y": y})
+        model.append(layer)
     torch.cuda.synchronize()
-    log(f"decode: {len(keep)} linears, {bytes_step / 1e6:.1f} MB per step")
+    return model
+
+
+# Dependency stages of one transformer layer: projections in a stage read the same
+# (or an independent) input; a stage needs the previous stage's output.
+LAYER_STAGES = (("q", "k", "v"), ("o",), ("gate", "up"), ("down",))
+
+
+def leg_decode(torch, args) -> dict:
+    """cfg3: 22 x 7 Q4_0 linears at M=1, each activation quantised to Q8_0 before its GEMV.
+
+    Three schedules of the same 154 quantise+GEMV tasks:
+      batched    -- one launch per step (the fp32 activations are quantised inside
+                    the GEMV workgroups); the cfg3 linears read independent
+                    activations, so the whole step is one batch;
+      staged     -- one launch per dependency stage (q/k/v, o, gate/up, down):
+                    88 launches per step, the order a real decode step needs;
+      per_linear -- a Q8_0 quantise kernel + a GEMV kernel per linear: 308 launches.
+    Each schedule is replayed as one HIP graph per step.
+    """
+    from qpu_xla_amd.kernels.ggml_q4_0 import Q4_0LinearBatch
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3)
+    model = _decode_model(torch, gen)
+    linears = [lin for layer in model for lin in layer]
+    bytes_step = sum(q4_linear_bytes(1, lin["k"], lin["n"]) for lin in linears)
+    fused_bytes = sum(lin["n"] * (lin["k"] // 32) * 18 + lin["k"] * 4 + lin["n"] * 4 for lin in linears)
+    log(f"decode: {len(linears)} linears, {bytes_step / 1e6:.1f} MB per step (fused kernel reads {fused_bytes / 1e6:.1f} MB)")
+    result = {"bytes_per_step": bytes_step}
+
+    def task(lin):
+        return {"x": lin["x"], "weight": lin["weight"], "destination": lin["y"]}
+
+    # batched: one launch per step.
+    stream = torch.cuda.Stream()
+    batch = Q4_0LinearBatch([task(lin) for lin in linears])
+    runner = Runner(torch, stream)
+    runner.add("qxt_q4_0_batch_launch", batch._handle, runner.handle)
     runner.run()
     torch.cuda.synchronize()
-    times = runner.kernel_times(repeats=2)
-    q4_times = times.get("q4_0_linear_kernel", [])
-    q8_times = times.get("q8_0_kernel", [])
+    times = runner.kernel_times(repeats=max(3, args.steps // 2))["q4_0_batch_kernel"]
     graph = runner.capture()
     wall_ms, event_ms = runner.timed_graph(graph, args.steps, args.warmup)
-    q4_avg_ms = float(np.mean(q4_times))
-    q4_avg_bytes = float(np.mean(q4_bytes_launches))
-    achieved = q4_avg_bytes / (q4_avg_ms * 1e-3) / 1e9
-    result = {
-        "bytes_per_step": bytes_step,
+    kernel_ms = float(np.mean(times))
+    result["batched"] = {
+        "launches_per_step": 1,
+        "work_items": batch.work_items,
         "ms_per_step_wall": wall_ms,
         "ms_per_step_events": event_ms,
         "gbs": bytes_step / (wall_ms * 1e-3) / 1e9,
-        "q4_linear_avg_us": q4_avg_ms * 1e3,
-        "q4_linear_avg_bytes": q4_avg_bytes,
-        "q4_linear_kernel_gbs": achieved,
-        "q4_linear_sum_us_per_step": float(np.sum(q4_times)) * 1e3 / 2,
-        "q8_0_avg_us": float(np.mean(q8_times)) * 1e3 if q8_times else None,
-        "launches_per_step": len(runner.calls),
+        "kernel_avg_us": kernel_ms * 1e3,
+        "kernel_min_us": float(np.min(times)) * 1e3,
+        "kernel_bytes_per_launch": fused_bytes,
+        "kernel_gbs": fused_bytes / (kernel_ms * 1e-3) / 1e9,
     }
-    del graph, keep
+    del graph
+    log(f"decode batched: {result['batched']}")
+
+    # staged: one batch per dependency stage.
+    stages = []
+    for layer in model:
+        by_name = {lin["name"]: lin for lin in layer}
+        for names in LAYER_STAGES:
+            stages.append(Q4_0LinearBatch([task(by_name[nm]) for nm in names]))
+    runner = Runner(torch, stream)
+    for st in stages:
+        runner.add("qxt_q4_0_batch_launch", st._handle, runner.handle)
+    runner.run()
+    torch.cuda.synchronize()
+    stimes = runner.kernel_times(repeats=2)["q4_0_batch_kernel"]
+    graph = runner.capture()
+    wall_ms, event_ms = runner.timed_graph(graph, args.steps, args.warmup)
+    result["staged"] = {
+        "launches_per_step": len(stages),
+        "ms_per_step_wall": wall_ms,
+        "ms_per_step_events": event_ms,
+        "gbs": bytes_step / (wall_ms * 1e-3) / 1e9,
+        "kernel_sum_us_per_step": float(np.sum(stimes)) * 1e3 / 2,
+    }
+    del graph
+    log(f"decode staged: {result['staged']}")
+
+    # per_linear: quantise kernel + GEMV kernel per linear.
+    runner = Runner(torch, stream)
+    for lin in linears:
+        x, xq, wq, y, k, n = lin["x"], lin["xq"], lin["weight"], lin["y"], lin["k"], lin["n"]
+        runner.add("qxt_quantize_q8_0", _p(x), _rs(x), _p(xq), _rs(xq), 1, k, runner.handle)
+        runner.add("qxt_ggml_q4_0_q8_0_linear", _p(xq), _rs(xq), _p(wq), _rs(wq), _p(y), _rs(y),
+                   1, k // 32, 0, 0, n, runner.handle)
+    runner.run()
+    torch.cuda.synchronize()
+    ptimes = runner.kernel_times(repeats=2)
+    graph = runner.capture()
+    wall_ms, event_ms = runner.timed_graph(graph, args.steps, args.warmup)
+    q4_times = ptimes.get("q4_0_linear_kernel", [])
+    result["per_linear"] = {
+        "launches_per_step": len(runner.calls),
+        "ms_per_step_wall": wall_ms,
+        "ms_per_step_events": event_ms,
+        "gbs": bytes_step / (wall_ms * 1e-3) / 1e9,
+        "q4_linear_avg_us": float(np.mean(q4_times)) * 1e3,
+        "q4_linear_kernel_gbs": bytes_step / len(linears) / (float(np.mean(q4_times)) * 1e-3) / 1e9,
+        "q8_0_avg_us": float(np.mean(ptimes.get("q8_0_kernel", [0.0]))) * 1e3,
+    }
+    del graph
+    log(f"decode per_linear: {result['per_linear']}")
+    batch.close()
+    for st in stages:
+        st.close()
+    del model, linears
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     return result
@@ -499,14 +578,15 @@ def main() -> int:
         log(f"cpu: {cpu} / {cpu_w8a8}")
 
     decode = out.get("decode")
+    head = decode["batched"] if decode else None
     line = {
         "metric": METRIC,
-        "value": decode["gbs"] if decode else None,
+        "value": head["gbs"] if head else None,
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": decode["ms_per_step_wall"] if decode else None,
+        "ms_per_step": head["ms_per_step_wall"] if head else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -515,23 +595,24 @@ def main() -> int:
         "config": {
             "workload": "cfg3: TinyLlama-1.1B decode step, 22 layers x 7 Q4_0xQ8_0 linears "
             "(q/o 2048x2048, k/v 2048->256, gate/up 2048->5632, down 5632->2048), M=1, "
-            "Q8_0 re-quantisation before each linear, one HIP graph per step",
+            "Q8_0 re-quantisation of each linear's activation, all 154 linears in one batched launch per step",
             "bytes_per_step": decode["bytes_per_step"] if decode else None,
-            "frac_hbm_peak": decode["gbs"] / PEAK_HBM_GBS if decode else None,
+            "frac_hbm_peak": head["gbs"] / PEAK_HBM_GBS if head else None,
+            "schedule": "batched",
         },
         "roofline": (
             {
                 "bound": "hbm",
-                "kernel": "q4_0_linear_kernel",
-                "achieved": decode["q4_linear_kernel_gbs"],
+                "kernel": "q4_0_batch_kernel",
+                "achieved": head["kernel_gbs"],
                 "peak": PEAK_HBM_GBS,
                 "unit": "GB/s",
-                "frac": decode["q4_linear_kernel_gbs"] / PEAK_HBM_GBS,
+                "frac": head["kernel_gbs"] / PEAK_HBM_GBS,
                 "traffic": None,
-                "bytes_per_launch": decode["q4_linear_avg_bytes"],
-                "avg_launch_us": decode["q4_linear_avg_us"],
+                "bytes_per_launch": head["kernel_bytes_per_launch"],
+                "avg_launch_us": head["kernel_avg_us"],
             }
-            if decode
+            if head
             else None
         ),
         "cpu_baseline": cpu,

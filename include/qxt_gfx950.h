@@ -163,6 +163,46 @@ int qxt_ggml_q4_0_q8_0_block_dots(const void *activation, size_t activation_row_
                                   uint32_t weight_column_start, uint32_t column_count,
                                   void *stream);
 
+/* One linear of a Q4_0 batch.  Exactly one of `x` (fp32 rows [rows, blocks*32]
+ * with 16-byte aligned rows, quantised to Q8_0 inside the kernel by the rule of
+ * qxt_quantize_q8_0) and `activation` (native Q8_0 blocks) is non-NULL; the
+ * other fields mean what they mean for qxt_ggml_q4_0_q8_0_linear.  Batched
+ * tasks need rows <= 4, blocks % 8 == 0 and 16-byte aligned weight rows. */
+typedef struct qxt_q4_0_task {
+    const float *x;
+    size_t x_row_stride;
+    const void *activation;
+    size_t activation_row_stride;
+    const void *weight;
+    size_t weight_row_stride;
+    float *destination;
+    size_t destination_row_stride;
+    uint32_t rows;
+    uint32_t blocks;
+    uint32_t weight_column_start;
+    uint32_t output_column_start;
+    uint32_t column_count;
+} qxt_q4_0_task;
+
+typedef struct qxt_q4_0_batch qxt_q4_0_batch;
+
+/* Prepare a batch of independent Q4_0 x Q8_0 linears that one kernel launch
+ * computes (e.g. every projection of a decode step); uploads a small task
+ * table with hipMalloc/hipMemcpy (synchronous).  The tensors the tasks point
+ * at must outlive the batch.  Replaces the prepared-linear handle
+ * qpu_llama_q4_0_linear_prepare (integrations/llama_cpp/include/qpu_llama_q4_0.h:63-66). */
+int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_batch **batch);
+
+/* Enqueue the whole batch on `stream` (one launch; graph-capturable).
+ * Replaces qpu_llama_q4_0_linear_submit (qpu_llama_q4_0.h:72-75). */
+int qxt_q4_0_batch_launch(const qxt_q4_0_batch *batch, void *stream);
+
+/* Number of workgroups one launch of the batch runs. No reference counterpart. */
+uint32_t qxt_q4_0_batch_work_items(const qxt_q4_0_batch *batch);
+
+/* Free the task table; replaces qpu_llama_q4_0_linear_destroy (qpu_llama_q4_0.h:67). */
+void qxt_q4_0_batch_destroy(qxt_q4_0_batch *batch);
+
 /* ------------------------------------------------------------------- W8A8 */
 
 /* acc[m, n] = sum_k a[m, k] * w(n, k), exact int32.  a: int8 [m, k] (row stride

@@ -3,23 +3,37 @@
 // Arithmetic (reference src/qpu_xla/kernels/ggml_q4_0.py:81-100 and the QPU
 // loop at :688-692): per 32-element block an exact int32 dot, then
 // c_b = fl32(fl32(float(dot_b) * dw_b) * da_b), summed in block order
-// ((0 + c_0) + c_1) + ...  This kernel reproduces that result bit for bit:
+// ((0 + c_0) + c_1) + ...  The kernel reproduces that result bit for bit.
 //
-//   phase 1  the workgroup stages the Q8_0 activation rows in LDS as int8
-//            words plus (fp32 scale, int32 element sum) per block;
-//   phase 2  every thread streams one "unit" of weights -- 8 consecutive
-//            blocks of one column, 144 bytes = 9 x 16-byte loads on the fast
-//            path -- computes the 8 block terms c_b with v_dot4_i32_i8 and
-//            writes them to LDS;
-//   phase 3  one thread per (row, column) adds that column's c_b in block
+// One workgroup (256 threads) owns a tile of `cpw` output columns of one
+// linear ("work item").  Because the weight rows of consecutive columns are
+// adjacent, the tile is one contiguous byte range of the [N, B, 18] weight
+// tensor, cut into "units" of 8 consecutive blocks of one column (144 bytes,
+// 9 x 16-byte loads on the fast path):
+//
+//   phase 0  each thread issues the loads of its U units into registers;
+//   phase 1  while those loads are in flight the workgroup stages the Q8_0
+//            activation rows in LDS (int8 words + fp32 scale + int32 element
+//            sum per block), either from native 34-byte blocks or by
+//            quantising fp32 activations itself (the Q8_0 rule of
+//            quantize_q8_0_split, examples/benchmark_llama_cpp_qpu_persistent_q4.py:42-53);
+//   phase 2  each unit yields 8 block terms c_b (v_dot4_i32_i8) into LDS;
+//   phase 3  one thread per (row, column) adds the column's c_b in block
 //            order and stores the fp32 result.
 //
-// Nibble codes enter the dot as unsigned 0..15; the "- 8" of every element
-// is applied once per block as -8 * sum(activation), which is exact in int32.
-// The fast path needs blocks % 8 == 0 and 16-byte aligned weight rows (true
-// for every K that is a multiple of 256); otherwise each thread takes one
-// block with 2-byte loads.
+// Nibble codes enter the dot as unsigned 0..15; the "- 8" of every element is
+// applied once per block as -8 * sum(activation), exact in int32.  The fast
+// path needs blocks % 8 == 0 and 16-byte aligned weight rows (every K that is
+// a multiple of 256); otherwise each thread takes one block with 2-byte loads.
+//
+// Entry points: a single linear (stateless, native Q8_0 activation), its
+// int32 block-dot debug twin, and a prepared batch of independent linears
+// launched as one grid (the decode step of a model whose projections read
+// separate activations).
+#include <algorithm>
+#include <new>
 #include <type_traits>
+#include <vector>
 
 #include "qxt_common.h"
 
@@ -29,16 +43,19 @@ namespace {
 constexpr int kThreads = 256;
 constexpr size_t kMaxLds = 64 * 1024;
 
-struct Q4Args {
-    const uint8_t *act;
-    size_t act_stride;
-    const uint8_t *w;
-    size_t w_stride;
-    float *dst;
-    size_t dst_stride;
-    int32_t *dots;  // non-null: debug mode, write int32 block dots instead of the sum
-    int rows, blocks, wcol0, ocol0, ncols;
-    int cpw;  // columns per workgroup
+struct Q4Task {
+    const float *x;        // fp32 activation rows, quantised in-kernel (batch only); else nullptr
+    const uint8_t *act;    // native Q8_0 blocks [rows, blocks, 34] when x == nullptr
+    const uint8_t *w;      // Q4_0 blocks [N, blocks, 18]
+    float *y;              // fp32 output
+    int32_t *dots;         // debug: int32 block dots [rows, ncols, blocks]
+    size_t x_stride, act_stride, w_stride, y_stride;  // row strides in bytes
+    int rows, blocks, wcol0, ocol0, ncols, cpw;
+};
+
+struct Q4Item {
+    int task;
+    int col_base;
 };
 
 // LDS geometry (in 32-bit words) for a row group of MR rows.
@@ -95,28 +112,59 @@ __device__ __forceinline__ int block_dot(const uint32_t (&qs)[4], const int *aq,
     return s - 8 * asum;
 }
 
-template <int MR, bool FAST, bool DOTS>
-__global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Args args) {
-    extern __shared__ int lds[];
-    const int B = args.blocks;
-    const Q4Lds geo(B, FAST);
-    int *aq = lds;                                  // [MR][aq_row]
-    int *ad = aq + MR * geo.aq_row;                 // [MR][ad_row]  (scale bits as float, sum)
-    float *cb = reinterpret_cast<float *>(ad + MR * geo.ad_row);  // [MR][cpw][cbs]
-
-    const int r0 = blockIdx.y * MR;
-    const int col_base = blockIdx.x * args.cpw;
-    const int tile_cols = min(args.cpw, args.ncols - col_base);
-
-    // ---- phase 1: stage the activation rows of this row group.
+// Stage the activation rows r0 .. r0+MR-1 of `t` into LDS (rows >= t.rows become zeros).
+template <int MR>
+__device__ __forceinline__ void stage_activation(const Q4Task &t, int r0, int *aq, int *ad, const Q4Lds &geo) {
+    const int B = t.blocks;
+    if (t.x != nullptr) {
+        // Quantise fp32 rows to Q8_0 in place: 8 lanes per block, float4 per lane.
+        // Same arithmetic as q8_0_kernel: d = absmax / 127, inv = 1 / d (0 when
+        // d == 0), q = clamp(rint(x * inv), +-127); the dot uses the fp16-rounded d.
+        for (int e = threadIdx.x; e < MR * B * 8; e += kThreads) {
+            const int r = e / (B * 8);
+            const int rem = e - r * B * 8;
+            const int b = rem >> 3;
+            const int l8 = rem & 7;
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (r0 + r < t.rows)
+                v = *reinterpret_cast<const float4 *>(reinterpret_cast<const uint8_t *>(t.x) + (r0 + r) * t.x_stride +
+                                                      (b * QK + l8 * 4) * 4);
+            float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+            amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
+            amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
+            amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
+            const float d = amax / 127.0f;
+            const float inv = (d != 0.0f) ? 1.0f / d : 0.0f;
+            int q[4];
+            const float xs[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int c = static_cast<int>(rintf(xs[i] * inv));
+                q[i] = c < -127 ? -127 : (c > 127 ? 127 : c);
+            }
+            int sum = q[0] + q[1] + q[2] + q[3];
+            sum += __shfl_xor(sum, 1, 8);
+            sum += __shfl_xor(sum, 2, 8);
+            sum += __shfl_xor(sum, 4, 8);
+            const uint32_t word = (static_cast<uint32_t>(q[0]) & 0xFFu) | ((static_cast<uint32_t>(q[1]) & 0xFFu) << 8) |
+                                  ((static_cast<uint32_t>(q[2]) & 0xFFu) << 16) |
+                                  ((static_cast<uint32_t>(q[3]) & 0xFFu) << 24);
+            aq[r * geo.aq_row + aq_index(b, l8)] = static_cast<int>(word);
+            if (l8 == 0) {
+                ad[r * geo.ad_row + ad_index(b)] = __float_as_int(half_bits_to_float(float_to_half_bits(d)));
+                ad[r * geo.ad_row + ad_index(b) + 1] = sum;
+            }
+        }
+        return;
+    }
     for (int idx = threadIdx.x; idx < MR * B; idx += kThreads) {
         const int r = idx / B;
         const int b = idx - r * B;
         int words[8] = {0, 0, 0, 0, 0, 0, 0, 0};
         float d = 0.0f;
         int sum = 0;
-        if (r0 + r < args.rows) {
-            const uint16_t *p = reinterpret_cast<const uint16_t *>(args.act + (r0 + r) * args.act_stride +
+        if (r0 + r < t.rows) {
+            const uint16_t *p = reinterpret_cast<const uint16_t *>(t.act + (r0 + r) * t.act_stride +
                                                                    static_cast<size_t>(b) * Q8_0_BYTES);
             d = half_bits_to_float(p[0]);
 #pragma unroll
@@ -132,94 +180,136 @@ __global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Args args) {
         ad[r * geo.ad_row + ad_index(b)] = __float_as_int(d);
         ad[r * geo.ad_row + ad_index(b) + 1] = sum;
     }
-    __syncthreads();
+}
 
-    // ---- phase 2: block terms.
-    if constexpr (FAST) {
-        const int G = B >> 3;
-        const int units = tile_cols * G;
-        for (int u = threadIdx.x; u < units; u += kThreads) {
+template <int U>
+__device__ __forceinline__ void load_units(const Q4Task &t, int col_base, int G, int units, int first,
+                                           uint32_t (&d)[U][36]) {
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+        const int u = first + j * kThreads + threadIdx.x;
+        if (u < units) {
             const int col = u / G;
             const int g = u - col * G;
-            const int n = args.wcol0 + col_base + col;
-            const uint4 *src = reinterpret_cast<const uint4 *>(args.w + static_cast<size_t>(n) * args.w_stride +
-                                                               static_cast<size_t>(g) * 144);
-            uint32_t d[36];
+            const uint4 *src = reinterpret_cast<const uint4 *>(
+                t.w + static_cast<size_t>(t.wcol0 + col_base + col) * t.w_stride + static_cast<size_t>(g) * 144);
 #pragma unroll
             for (int v = 0; v < 9; ++v) {
                 const uint4 x = src[v];
-                d[4 * v + 0] = x.x;
-                d[4 * v + 1] = x.y;
-                d[4 * v + 2] = x.z;
-                d[4 * v + 3] = x.w;
+                d[j][4 * v + 0] = x.x;
+                d[j][4 * v + 1] = x.y;
+                d[j][4 * v + 2] = x.z;
+                d[j][4 * v + 3] = x.w;
             }
-            float terms[MR][8];
-            int idots[MR][8];
-            auto do_block = [&](auto ic) {
-                constexpr int I = decltype(ic)::value;
-                uint32_t sbits, qs[4];
-                unit_block<I>(d, sbits, qs);
-                const float dw = half_bits_to_float(sbits);
-                const int b = g * 8 + I;
+        }
+    }
+}
+
+template <int MR, int U, bool FAST, bool DOTS, bool BATCH>
+__global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Task single, const Q4Task *__restrict__ tasks,
+                                                               const Q4Item *__restrict__ items) {
+    extern __shared__ int lds[];
+    Q4Task t;
+    int col_base, r0;
+    if constexpr (BATCH) {
+        const Q4Item item = items[blockIdx.x];
+        t = tasks[item.task];
+        col_base = item.col_base;
+        r0 = 0;
+    } else {
+        t = single;
+        col_base = blockIdx.x * t.cpw;
+        r0 = blockIdx.y * MR;
+    }
+    const int B = t.blocks;
+    const Q4Lds geo(B, FAST);
+    int *aq = lds;                                                 // [MR][aq_row]
+    int *ad = aq + MR * geo.aq_row;                                // [MR][ad_row] (fp32 scale bits, sum)
+    float *cb = reinterpret_cast<float *>(ad + MR * geo.ad_row);  // [MR][cpw][cbs]
+    const int tile_cols = min(t.cpw, t.ncols - col_base);
+
+    const int G = FAST ? (B >> 3) : B;
+    const int units = tile_cols * G;
+    uint32_t wr[FAST ? U : 1][36];
+    if constexpr (FAST) load_units<U>(t, col_base, G, units, 0, wr);
+
+    stage_activation<MR>(t, r0, aq, ad, geo);
+    __syncthreads();
+
+    if constexpr (FAST) {
+        for (int first = 0; first < units; first += U * kThreads) {
+            if (first > 0) load_units<U>(t, col_base, G, units, first, wr);
+#pragma unroll
+            for (int j = 0; j < U; ++j) {
+                const int u = first + j * kThreads + threadIdx.x;
+                if (u >= units) continue;
+                const int col = u / G;
+                const int g = u - col * G;
+                float terms[MR][8];
+                int idots[MR][8];
+                auto do_block = [&](auto ic) {
+                    constexpr int I = decltype(ic)::value;
+                    uint32_t sbits, qs[4];
+                    unit_block<I>(wr[j], sbits, qs);
+                    const float dw = half_bits_to_float(sbits);
+                    const int b = g * 8 + I;
+#pragma unroll
+                    for (int r = 0; r < MR; ++r) {
+                        const int2 ds = *reinterpret_cast<const int2 *>(ad + r * geo.ad_row + ad_index(b));
+                        const int dot = block_dot(qs, aq + r * geo.aq_row + aq_index(b, 0), ds.y);
+                        idots[r][I] = dot;
+                        float v = static_cast<float>(dot) * dw;
+                        v = v * __int_as_float(ds.x);
+                        terms[r][I] = v;
+                    }
+                };
+                do_block(std::integral_constant<int, 0>{});
+                do_block(std::integral_constant<int, 1>{});
+                do_block(std::integral_constant<int, 2>{});
+                do_block(std::integral_constant<int, 3>{});
+                do_block(std::integral_constant<int, 4>{});
+                do_block(std::integral_constant<int, 5>{});
+                do_block(std::integral_constant<int, 6>{});
+                do_block(std::integral_constant<int, 7>{});
 #pragma unroll
                 for (int r = 0; r < MR; ++r) {
-                    const int *arow = aq + r * geo.aq_row + aq_index(b, 0);
-                    const int2 ds = *reinterpret_cast<const int2 *>(ad + r * geo.ad_row + ad_index(b));
-                    const int dot = block_dot(qs, arow, ds.y);
-                    idots[r][I] = dot;
-                    float t = static_cast<float>(dot) * dw;
-                    t = t * __int_as_float(ds.x);
-                    terms[r][I] = t;
-                }
-            };
-            do_block(std::integral_constant<int, 0>{});
-            do_block(std::integral_constant<int, 1>{});
-            do_block(std::integral_constant<int, 2>{});
-            do_block(std::integral_constant<int, 3>{});
-            do_block(std::integral_constant<int, 4>{});
-            do_block(std::integral_constant<int, 5>{});
-            do_block(std::integral_constant<int, 6>{});
-            do_block(std::integral_constant<int, 7>{});
+                    if constexpr (DOTS) {
+                        if (r0 + r < t.rows) {
+                            int32_t *out =
+                                t.dots + (static_cast<size_t>(r0 + r) * t.ncols + col_base + col) * B + g * 8;
 #pragma unroll
-            for (int r = 0; r < MR; ++r) {
-                if constexpr (DOTS) {
-                    if (r0 + r < args.rows) {
-                        int32_t *out = args.dots + (static_cast<size_t>(r0 + r) * args.ncols + col_base + col) * B +
-                                       g * 8;
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) out[i] = idots[r][i];
+                            for (int i = 0; i < 8; ++i) out[i] = idots[r][i];
+                        }
+                    } else {
+                        float4 *c4 = reinterpret_cast<float4 *>(cb + (r * t.cpw + col) * geo.cbs + g * 8);
+                        c4[0] = make_float4(terms[r][0], terms[r][1], terms[r][2], terms[r][3]);
+                        c4[1] = make_float4(terms[r][4], terms[r][5], terms[r][6], terms[r][7]);
                     }
-                } else {
-                    float4 *c4 = reinterpret_cast<float4 *>(cb + (r * args.cpw + col) * geo.cbs + g * 8);
-                    c4[0] = make_float4(terms[r][0], terms[r][1], terms[r][2], terms[r][3]);
-                    c4[1] = make_float4(terms[r][4], terms[r][5], terms[r][6], terms[r][7]);
                 }
             }
         }
     } else {
-        const int units = tile_cols * B;
         for (int u = threadIdx.x; u < units; u += kThreads) {
             const int col = u / B;
             const int b = u - col * B;
-            const int n = args.wcol0 + col_base + col;
-            const uint16_t *p = reinterpret_cast<const uint16_t *>(args.w + static_cast<size_t>(n) * args.w_stride +
+            const uint16_t *p = reinterpret_cast<const uint16_t *>(t.w + static_cast<size_t>(t.wcol0 + col_base + col) *
+                                                                             t.w_stride +
                                                                    static_cast<size_t>(b) * Q4_0_BYTES);
             const float dw = half_bits_to_float(p[0]);
             uint32_t qs[4];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) qs[t] = static_cast<uint32_t>(p[1 + 2 * t]) | (static_cast<uint32_t>(p[2 + 2 * t]) << 16);
+            for (int q = 0; q < 4; ++q)
+                qs[q] = static_cast<uint32_t>(p[1 + 2 * q]) | (static_cast<uint32_t>(p[2 + 2 * q]) << 16);
 #pragma unroll
             for (int r = 0; r < MR; ++r) {
-                const int *arow = aq + r * geo.aq_row + aq_index(b, 0);
                 const int2 ds = *reinterpret_cast<const int2 *>(ad + r * geo.ad_row + ad_index(b));
-                const int dot = block_dot(qs, arow, ds.y);
+                const int dot = block_dot(qs, aq + r * geo.aq_row + aq_index(b, 0), ds.y);
                 if constexpr (DOTS) {
-                    if (r0 + r < args.rows)
-                        args.dots[(static_cast<size_t>(r0 + r) * args.ncols + col_base + col) * B + b] = dot;
+                    if (r0 + r < t.rows) t.dots[(static_cast<size_t>(r0 + r) * t.ncols + col_base + col) * B + b] = dot;
                 } else {
-                    float t = static_cast<float>(dot) * dw;
-                    t = t * __int_as_float(ds.x);
-                    cb[(r * args.cpw + col) * geo.cbs + b] = t;
+                    float v = static_cast<float>(dot) * dw;
+                    v = v * __int_as_float(ds.x);
+                    cb[(r * t.cpw + col) * geo.cbs + b] = v;
                 }
             }
         }
@@ -228,11 +318,11 @@ __global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Args args) {
     __syncthreads();
 
     // ---- phase 3: in-order fp32 sum per (row, column).
-    for (int t = threadIdx.x; t < MR * tile_cols; t += kThreads) {
-        const int r = t / tile_cols;
-        const int col = t - r * tile_cols;
-        if (r0 + r >= args.rows) continue;
-        const float *c = cb + (r * args.cpw + col) * geo.cbs;
+    for (int k = threadIdx.x; k < MR * tile_cols; k += kThreads) {
+        const int r = k / tile_cols;
+        const int col = k - r * tile_cols;
+        if (r0 + r >= t.rows) continue;
+        const float *c = cb + (r * t.cpw + col) * geo.cbs;
         float acc = 0.0f;
         if constexpr (FAST) {
             for (int b = 0; b < B; b += 4) {
@@ -245,36 +335,57 @@ __global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Args args) {
         } else {
             for (int b = 0; b < B; ++b) acc += c[b];
         }
-        float *out = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(args.dst) + (r0 + r) * args.dst_stride);
-        out[args.ocol0 + col_base + col] = acc;
+        float *out = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(t.y) + (r0 + r) * t.y_stride);
+        out[t.ocol0 + col_base + col] = acc;
     }
 }
 
+// Units each thread owns per round on the fast path (more bytes in flight at M = 1).
+constexpr int units_per_thread(int mr) { return mr == 1 ? 2 : 1; }
+
+bool fast_path(const Q4Task &t) { return t.blocks % 8 == 0 && aligned(t.w, 16) && t.w_stride % 16 == 0; }
+
+// Columns per workgroup and dynamic LDS bytes for a task, or an error status.
+int plan_task(Q4Task &t, int mr, bool fast, bool dots, size_t *lds) {
+    const Q4Lds geo(t.blocks, fast);
+    const int units_per_col = fast ? t.blocks / 8 : t.blocks;
+    const int per_round = kThreads * (fast ? units_per_thread(mr) : 1);
+    int cpw = units_per_col >= per_round ? 1 : per_round / units_per_col;
+    cpw = std::max(1, std::min(cpw, t.ncols));
+    while (cpw > 1 && geo.words(mr, dots ? 0 : cpw) * 4 > kMaxLds) --cpw;
+    *lds = geo.words(mr, dots ? 0 : cpw) * 4;
+    if (*lds > kMaxLds)
+        return fail(QXT_CAPABILITY_MISSING, "q4_0 linear: K=%d needs %zu bytes of LDS (> %zu)", t.blocks * 32, *lds,
+                    kMaxLds);
+    t.cpw = cpw;
+    return QXT_OK;
+}
+
 template <int MR, bool DOTS>
-int launch_q4(Q4Args args, bool fast, hipStream_t stream) {
-    const Q4Lds geo(args.blocks, fast);
-    const int units_per_col = fast ? args.blocks / 8 : args.blocks;
-    int cpw = units_per_col >= kThreads ? 1 : kThreads / units_per_col;
-    while (cpw > 1 && geo.words(MR, DOTS ? 0 : cpw) * 4 > kMaxLds) --cpw;
-    const size_t lds = geo.words(MR, DOTS ? 0 : cpw) * 4;
-    if (lds > kMaxLds)
-        return fail(QXT_CAPABILITY_MISSING, "q4_0 linear: K=%d needs %zu bytes of LDS (> %zu)", args.blocks * 32,
-                    lds, kMaxLds);
-    args.cpw = cpw;
-    dim3 grid((args.ncols + cpw - 1) / cpw, (args.rows + MR - 1) / MR, 1);
-    return launch(DOTS ? "q4_0_block_dots_kernel" : "q4_0_linear_kernel",
-                  fast ? q4_0_linear_kernel<MR, true, DOTS> : q4_0_linear_kernel<MR, false, DOTS>, grid,
-                  dim3(kThreads), lds, stream, args);
+int launch_single(Q4Task t, hipStream_t stream) {
+    const bool fast = fast_path(t);
+    size_t lds = 0;
+    int rc = plan_task(t, MR, fast, DOTS, &lds);
+    if (rc != QXT_OK) return rc;
+    dim3 grid((t.ncols + t.cpw - 1) / t.cpw, (t.rows + MR - 1) / MR, 1);
+    constexpr int U = units_per_thread(MR);
+    const char *name = DOTS ? "q4_0_block_dots_kernel" : "q4_0_linear_kernel";
+    const Q4Task *no_tasks = nullptr;
+    const Q4Item *no_items = nullptr;
+    if (fast)
+        return launch(name, q4_0_linear_kernel<MR, U, true, DOTS, false>, grid, dim3(kThreads), lds, stream, t,
+                      no_tasks, no_items);
+    return launch(name, q4_0_linear_kernel<MR, 1, false, DOTS, false>, grid, dim3(kThreads), lds, stream, t, no_tasks,
+                  no_items);
 }
 
 template <bool DOTS>
-int dispatch_q4(const Q4Args &args, hipStream_t stream) {
-    const bool fast = args.blocks % 8 == 0 && aligned(args.w, 16) && args.w_stride % 16 == 0;
-    switch (args.rows >= 4 ? 4 : args.rows) {
-        case 1: return launch_q4<1, DOTS>(args, fast, stream);
-        case 2: return launch_q4<2, DOTS>(args, fast, stream);
-        case 3: return launch_q4<3, DOTS>(args, fast, stream);
-        default: return launch_q4<4, DOTS>(args, fast, stream);
+int dispatch_single(const Q4Task &t, hipStream_t stream) {
+    switch (t.rows >= 4 ? 4 : t.rows) {
+        case 1: return launch_single<1, DOTS>(t, stream);
+        case 2: return launch_single<2, DOTS>(t, stream);
+        case 3: return launch_single<3, DOTS>(t, stream);
+        default: return launch_single<4, DOTS>(t, stream);
     }
 }
 
@@ -297,6 +408,16 @@ int validate_q4(const void *activation, size_t activation_row_stride, const void
 
 using namespace qxt;
 
+struct qxt_q4_0_batch {
+    void *device_tables = nullptr;  // [Q4Task x count][Q4Item x items]
+    const Q4Task *tasks = nullptr;
+    const Q4Item *items = nullptr;
+    uint32_t task_count = 0;
+    uint32_t item_count = 0;
+    int mr = 1;
+    size_t lds = 0;
+};
+
 extern "C" {
 
 int qxt_ggml_q4_0_q8_0_linear(const void *activation, size_t activation_row_stride, const void *weight,
@@ -313,20 +434,19 @@ int qxt_ggml_q4_0_q8_0_linear(const void *activation, size_t activation_row_stri
         return fail(QXT_INVALID_ARGUMENT, "q4_0 linear: column range overflows");
     rc = injected(QXT_FAIL_SUBMISSION);
     if (rc != QXT_OK) return rc;
-    Q4Args args{static_cast<const uint8_t *>(activation),
-                activation_row_stride,
-                static_cast<const uint8_t *>(weight),
-                weight_row_stride,
-                destination,
-                destination_row_stride,
-                nullptr,
-                static_cast<int>(rows),
-                static_cast<int>(blocks),
-                static_cast<int>(weight_column_start),
-                static_cast<int>(output_column_start),
-                static_cast<int>(column_count),
-                0};
-    return dispatch_q4<false>(args, as_stream(stream));
+    Q4Task t{};
+    t.act = static_cast<const uint8_t *>(activation);
+    t.act_stride = activation_row_stride;
+    t.w = static_cast<const uint8_t *>(weight);
+    t.w_stride = weight_row_stride;
+    t.y = destination;
+    t.y_stride = destination_row_stride;
+    t.rows = static_cast<int>(rows);
+    t.blocks = static_cast<int>(blocks);
+    t.wcol0 = static_cast<int>(weight_column_start);
+    t.ocol0 = static_cast<int>(output_column_start);
+    t.ncols = static_cast<int>(column_count);
+    return dispatch_single<false>(t, as_stream(stream));
 }
 
 int qxt_ggml_q4_0_q8_0_block_dots(const void *activation, size_t activation_row_stride, const void *weight,
@@ -339,20 +459,122 @@ int qxt_ggml_q4_0_q8_0_block_dots(const void *activation, size_t activation_row_
         return fail(QXT_INVALID_ARGUMENT, "q4_0 block dots: column range overflows");
     rc = injected(QXT_FAIL_SUBMISSION);
     if (rc != QXT_OK) return rc;
-    Q4Args args{static_cast<const uint8_t *>(activation),
-                activation_row_stride,
-                static_cast<const uint8_t *>(weight),
-                weight_row_stride,
-                nullptr,
-                0,
-                dots,
-                static_cast<int>(rows),
-                static_cast<int>(blocks),
-                static_cast<int>(weight_column_start),
-                0,
-                static_cast<int>(column_count),
-                0};
-    return dispatch_q4<true>(args, as_stream(stream));
+    Q4Task t{};
+    t.act = static_cast<const uint8_t *>(activation);
+    t.act_stride = activation_row_stride;
+    t.w = static_cast<const uint8_t *>(weight);
+    t.w_stride = weight_row_stride;
+    t.dots = dots;
+    t.rows = static_cast<int>(rows);
+    t.blocks = static_cast<int>(blocks);
+    t.wcol0 = static_cast<int>(weight_column_start);
+    t.ncols = static_cast<int>(column_count);
+    return dispatch_single<true>(t, as_stream(stream));
+}
+
+int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_batch **out) {
+    if (out == nullptr) return fail(QXT_INVALID_ARGUMENT, "q4_0 batch: null output handle");
+    *out = nullptr;
+    if (tasks == nullptr || count == 0) return fail(QXT_INVALID_ARGUMENT, "q4_0 batch: no tasks");
+    std::vector<Q4Task> host(count);
+    uint32_t max_rows = 1;
+    for (uint32_t i = 0; i < count; ++i) {
+        const qxt_q4_0_task &d = tasks[i];
+        if ((d.x == nullptr) == (d.activation == nullptr))
+            return fail(QXT_INVALID_ARGUMENT, "q4_0 batch task %u: give exactly one of x and activation", i);
+        const void *act = d.x != nullptr ? static_cast<const void *>(d.x) : d.activation;
+        const size_t act_stride =
+            d.x != nullptr ? static_cast<size_t>(d.blocks) * Q8_0_BYTES : d.activation_row_stride;
+        int rc = validate_q4(act, act_stride, d.weight, d.weight_row_stride, d.rows, d.blocks, d.column_count);
+        if (rc != QXT_OK) return rc;
+        if (d.rows > 4) return fail(QXT_INVALID_ARGUMENT, "q4_0 batch task %u: at most 4 rows per task", i);
+        if (d.x != nullptr && (!aligned(d.x, 16) || d.x_row_stride % 16 ||
+                               d.x_row_stride < static_cast<size_t>(d.blocks) * QK * sizeof(float)))
+            return fail(QXT_INVALID_ARGUMENT, "q4_0 batch task %u: fp32 activation rows must be 16-byte aligned", i);
+        if (d.destination == nullptr || !aligned(d.destination, 4) || d.destination_row_stride % 4 ||
+            d.destination_row_stride < (static_cast<size_t>(d.output_column_start) + d.column_count) * sizeof(float))
+            return fail(QXT_INVALID_ARGUMENT, "q4_0 batch task %u: bad destination", i);
+        if (static_cast<uint64_t>(d.weight_column_start) + d.column_count > (1ull << 31) ||
+            static_cast<uint64_t>(d.output_column_start) + d.column_count > (1ull << 31))
+            return fail(QXT_INVALID_ARGUMENT, "q4_0 batch task %u: column range overflows", i);
+        Q4Task t{};
+        t.x = d.x;
+        t.x_stride = d.x_row_stride;
+        t.act = static_cast<const uint8_t *>(d.activation);
+        t.act_stride = d.activation_row_stride;
+        t.w = static_cast<const uint8_t *>(d.weight);
+        t.w_stride = d.weight_row_stride;
+        t.y = d.destination;
+        t.y_stride = d.destination_row_stride;
+        t.rows = static_cast<int>(d.rows);
+        t.blocks = static_cast<int>(d.blocks);
+        t.wcol0 = static_cast<int>(d.weight_column_start);
+        t.ocol0 = static_cast<int>(d.output_column_start);
+        t.ncols = static_cast<int>(d.column_count);
+        if (!fast_path(t))
+            return fail(QXT_INVALID_ARGUMENT, "q4_0 batch task %u: needs K %% 256 == 0 and 16-byte aligned weight rows",
+                        i);
+        host[i] = t;
+        max_rows = std::max(max_rows, d.rows);
+    }
+    const int mr = max_rows == 1 ? 1 : 4;
+    size_t lds = 0;
+    std::vector<Q4Item> items;
+    for (uint32_t i = 0; i < count; ++i) {
+        size_t task_lds = 0;
+        int rc = plan_task(host[i], mr, true, false, &task_lds);
+        if (rc != QXT_OK) return rc;
+        lds = std::max(lds, task_lds);
+        for (int c = 0; c < host[i].ncols; c += host[i].cpw) items.push_back({static_cast<int>(i), c});
+    }
+    if (items.size() > 0x7FFFFFFFu) return fail(QXT_INVALID_ARGUMENT, "q4_0 batch: too many work items");
+    int rc = injected(QXT_FAIL_ALLOCATION);
+    if (rc != QXT_OK) return rc;
+    auto *batch = new (std::nothrow) qxt_q4_0_batch();
+    if (batch == nullptr) return fail(QXT_ALLOCATION_FAILED, "q4_0 batch: host allocation failed");
+    const size_t task_bytes = (sizeof(Q4Task) * count + 255) & ~size_t(255);
+    const size_t bytes = task_bytes + sizeof(Q4Item) * items.size();
+    if (hipMalloc(&batch->device_tables, bytes) != hipSuccess) {
+        delete batch;
+        return fail(QXT_ALLOCATION_FAILED, "q4_0 batch: hipMalloc of %zu bytes failed", bytes);
+    }
+    auto *base = static_cast<uint8_t *>(batch->device_tables);
+    if (hipMemcpy(base, host.data(), sizeof(Q4Task) * count, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(base + task_bytes, items.data(), sizeof(Q4Item) * items.size(), hipMemcpyHostToDevice) !=
+            hipSuccess) {
+        (void)hipFree(batch->device_tables);
+        delete batch;
+        return fail(QXT_IO_FAILED, "q4_0 batch: upload of the task tables failed");
+    }
+    batch->tasks = reinterpret_cast<const Q4Task *>(base);
+    batch->items = reinterpret_cast<const Q4Item *>(base + task_bytes);
+    batch->task_count = count;
+    batch->item_count = static_cast<uint32_t>(items.size());
+    batch->mr = mr;
+    batch->lds = lds;
+    *out = batch;
+    return QXT_OK;
+}
+
+int qxt_q4_0_batch_launch(const qxt_q4_0_batch *batch, void *stream) {
+    if (batch == nullptr) return fail(QXT_INVALID_ARGUMENT, "q4_0 batch: null handle");
+    int rc = injected(QXT_FAIL_SUBMISSION);
+    if (rc != QXT_OK) return rc;
+    const dim3 grid(batch->item_count, 1, 1);
+    const Q4Task none{};
+    if (batch->mr == 1)
+        return launch("q4_0_batch_kernel", q4_0_linear_kernel<1, units_per_thread(1), true, false, true>, grid,
+                      dim3(kThreads), batch->lds, as_stream(stream), none, batch->tasks, batch->items);
+    return launch("q4_0_batch_kernel", q4_0_linear_kernel<4, units_per_thread(4), true, false, true>, grid,
+                  dim3(kThreads), batch->lds, as_stream(stream), none, batch->tasks, batch->items);
+}
+
+uint32_t qxt_q4_0_batch_work_items(const qxt_q4_0_batch *batch) { return batch == nullptr ? 0 : batch->item_count; }
+
+void qxt_q4_0_batch_destroy(qxt_q4_0_batch *batch) {
+    if (batch == nullptr) return;
+    if (batch->device_tables != nullptr) (void)hipFree(batch->device_tables);
+    delete batch;
 }
 
 }  // extern "C"

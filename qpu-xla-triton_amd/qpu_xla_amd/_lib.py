@@ -56,6 +56,26 @@ class LaunchRecord(Structure):
     _fields_ = [("kernel", c_char * 48), ("ms", ctypes.c_float)]
 
 
+class Q4Task(Structure):
+    """``qxt_q4_0_task``: one linear of a Q4_0 batch."""
+
+    _fields_ = [
+        ("x", c_void_p),
+        ("x_row_stride", c_size_t),
+        ("activation", c_void_p),
+        ("activation_row_stride", c_size_t),
+        ("weight", c_void_p),
+        ("weight_row_stride", c_size_t),
+        ("destination", c_void_p),
+        ("destination_row_stride", c_size_t),
+        ("rows", c_uint32),
+        ("blocks", c_uint32),
+        ("weight_column_start", c_uint32),
+        ("output_column_start", c_uint32),
+        ("column_count", c_uint32),
+    ]
+
+
 _P = c_void_p
 _SZ = c_size_t
 _U = c_uint32
@@ -75,6 +95,10 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "qxt_quantize_q4_0": (c_int, [_P, _SZ, _P, _SZ, _U, _U, _P]),
     "qxt_ggml_q4_0_q8_0_linear": (c_int, [_P, _SZ, _P, _SZ, _P, _SZ, _U, _U, _U, _U, _U, _P]),
     "qxt_ggml_q4_0_q8_0_block_dots": (c_int, [_P, _SZ, _P, _SZ, _P, _U, _U, _U, _U, _P]),
+    "qxt_q4_0_batch_prepare": (c_int, [POINTER(Q4Task), _U, POINTER(c_void_p)]),
+    "qxt_q4_0_batch_launch": (c_int, [_P, _P]),
+    "qxt_q4_0_batch_work_items": (_U, [_P]),
+    "qxt_q4_0_batch_destroy": (None, [_P]),
     "qxt_w8a8_gemm_i32": (c_int, [_P, _SZ, _P, _SZ, _P, _SZ, _U, _U, _U, _U, _P]),
     "qxt_w8a8_gemm_dequantize": (c_int, [_P, _SZ, _P, _SZ, _P, _P, _P, _P, _SZ, _U, _U, _U, _U, _P]),
     "qxt_w8a8_dequantize": (c_int, [_P, _SZ, _P, _P, _P, _P, _SZ, _U, _U, _P]),

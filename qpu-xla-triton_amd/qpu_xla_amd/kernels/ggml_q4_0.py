@@ -205,3 +205,97 @@ def ggml_q4_0_q8_0_block_dots(
         rows, blocks, weight_column_start, column_count, stream_handle(stream),
     )
     return dots
+
+
+class Q4_0LinearBatch:
+    """Independent Q4_0 x Q8_0 linears computed by one kernel launch.
+
+    Each task is a dict with ``weight`` (uint8 [N, B, 18]), ``destination``
+    (float32 [rows, >= N]) and exactly one of ``x`` (float32 [rows, B*32]:
+    quantised to Q8_0 inside the kernel, same rule as ``quantize_q8_0``) or
+    ``activation`` (native Q8_0 uint8 [rows, B, 34]); optional
+    ``weight_column_start``, ``output_column_start`` and ``column_count``.
+    The batch keeps references to every tensor; their storage must not be
+    reallocated while the batch is alive (launches read the pointers
+    captured at construction).  This is the prepared-handle shape of the
+    reference's ``qpu_llama_q4_0_linear_prepare`` / ``_submit``
+    (integrations/llama_cpp/include/qpu_llama_q4_0.h:63-75).
+    """
+
+    def __init__(self, tasks: list[dict]) -> None:
+        import ctypes
+
+        if not tasks:
+            raise ValueError("Q4_0LinearBatch needs at least one task")
+        self._tensors = []
+        table = (_lib.Q4Task * len(tasks))()
+        for i, spec in enumerate(tasks):
+            weight = spec["weight"]
+            destination = spec["destination"]
+            x = spec.get("x")
+            activation = spec.get("activation")
+            if (x is None) == (activation is None):
+                raise ValueError("each task needs exactly one of 'x' and 'activation'")
+            if weight.dtype != torch.uint8 or weight.dim() != 3 or weight.shape[2] != Q4_0_BLOCK_BYTES:
+                raise ValueError("task weight must be uint8 [N, B, 18]")
+            if not weight.is_contiguous() or destination.dtype != torch.float32 or not rows_are_dense(destination):
+                raise ValueError("task weight must be contiguous and destination float32 with contiguous rows")
+            blocks = weight.shape[1]
+            source = x if x is not None else activation
+            rows = source.shape[0]
+            wcol0 = int(spec.get("weight_column_start", 0))
+            ocol0 = int(spec.get("output_column_start", 0))
+            ncols = int(spec.get("column_count", weight.shape[0] - wcol0))
+            if wcol0 < 0 or wcol0 + ncols > weight.shape[0] or ocol0 < 0 or ocol0 + ncols > destination.shape[1]:
+                raise ValueError("task column range out of bounds")
+            if destination.shape[0] != rows:
+                raise ValueError("task destination rows differ from the activation rows")
+            if x is not None:
+                if x.dtype != torch.float32 or x.dim() != 2 or x.shape[1] != blocks * Q4_0_BLOCK_ELEMENTS or not rows_are_dense(x):
+                    raise ValueError("task x must be float32 [rows, K] with contiguous rows")
+                table[i].x = x.data_ptr()
+                table[i].x_row_stride = row_stride(x)
+            else:
+                if activation.dtype != torch.uint8 or tuple(activation.shape[1:]) != (blocks, Q8_0_BLOCK_BYTES) or not activation.is_contiguous():
+                    raise ValueError("task activation must be contiguous uint8 [rows, B, 34]")
+                table[i].activation = activation.data_ptr()
+                table[i].activation_row_stride = row_stride(activation)
+            require_gpu("Q4_0LinearBatch", source, weight, destination)
+            table[i].weight = weight.data_ptr()
+            table[i].weight_row_stride = row_stride(weight)
+            table[i].destination = destination.data_ptr()
+            table[i].destination_row_stride = row_stride(destination)
+            table[i].rows = rows
+            table[i].blocks = blocks
+            table[i].weight_column_start = wcol0
+            table[i].output_column_start = ocol0
+            table[i].column_count = ncols
+            self._tensors.extend(t for t in (x, activation, weight, destination) if t is not None)
+        handle = ctypes.c_void_p()
+        _lib.check(_lib.load().qxt_q4_0_batch_prepare(table, len(tasks), ctypes.byref(handle)))
+        self._handle = handle
+        self.task_count = len(tasks)
+        self.work_items = int(_lib.load().qxt_q4_0_batch_work_items(handle))
+
+    def launch(self, stream: Any = None) -> None:
+        if self._handle is None:
+            raise RuntimeError("Q4_0LinearBatch is closed")
+        _lib.call("qxt_q4_0_batch_launch", self._handle, stream_handle(stream))
+
+    def close(self) -> None:
+        if self._handle is not None:
+            _lib.load().qxt_q4_0_batch_destroy(self._handle)
+            self._handle = None
+            self._tensors = []
+
+    def __enter__(self) -> "Q4_0LinearBatch":
+        return self
+
+    def __exit__(self, *exc: object) -> None:
+        self.close()
+
+    def __del__(self) -> None:
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001 - interpreter shutdown
+            pass

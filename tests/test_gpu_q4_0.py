@@ -165,3 +165,72 @@ def test_baseline_configs_end_to_end_bit_exact(seed: int, rows: int, k: int, n: 
     np.testing.assert_array_equal(out, expected)
     # The north-star tolerance (rel 1e-5 of max|ref|) holds a fortiori.
     assert np.abs(out - expected).max() <= 1e-5 * np.abs(expected).max()
+
+
+def _batch_case(seed: int, shapes, fused_every: int = 2):
+    """Tasks over (rows, k, n, wcol0, ncols) with alternating fp32 (fused) / native Q8_0 inputs."""
+    rng = np.random.default_rng(seed)
+    tasks, expected = [], []
+    for i, (rows, k, n, wcol0, ncols) in enumerate(shapes):
+        w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+        x = rng.standard_normal((rows, k), dtype=np.float32)
+        x[0, :32] = 0.0  # an all-zero activation block
+        wq = oracle.quantize_q4_0_blocks(w)
+        xq = oracle.quantize_q8_0_blocks(x)
+        dest = torch.full((rows, ncols + 16), float(SENTINEL), device="cuda")
+        task = {"weight": dev(wq), "destination": dest, "weight_column_start": wcol0,
+                "output_column_start": 16, "column_count": ncols}
+        if i % fused_every == 0:
+            task["x"] = dev(x)
+        else:
+            task["activation"] = dev(xq)
+        tasks.append(task)
+        expected.append(oracle.q4_0_q8_0_reference(xq, wq[wcol0:wcol0 + ncols]))
+    return tasks, expected
+
+
+def _check_batch(tasks, expected) -> None:
+    for task, want in zip(tasks, expected):
+        out = task["destination"].cpu().numpy()
+        np.testing.assert_array_equal(out[:, :16], SENTINEL)
+        np.testing.assert_array_equal(out[:, 16:], want)
+
+
+def test_batch_m1_mixed_shapes_bit_exact() -> None:
+    shapes = [(1, 2048, 2048, 0, 2048), (1, 2048, 256, 0, 256), (1, 5632, 2048, 0, 2048),
+              (1, 2048, 5632, 0, 5632), (1, 256, 48, 16, 17), (1, 4096, 100, 3, 90)]
+    tasks, expected = _batch_case(31, shapes)
+    with q4.Q4_0LinearBatch(tasks) as batch:
+        assert batch.task_count == len(shapes) and batch.work_items > len(shapes)
+        batch.launch()
+        torch.cuda.synchronize()
+        _check_batch(tasks, expected)
+        for t in tasks:
+            t["destination"][:, 16:] = -1.0
+        batch.launch()  # a second launch of the same prepared batch
+        torch.cuda.synchronize()
+        _check_batch(tasks, expected)
+
+
+def test_batch_small_m_bit_exact() -> None:
+    shapes = [(4, 4096, 64, 0, 64), (2, 2048, 40, 8, 32), (3, 256, 16, 0, 16), (1, 512, 33, 0, 33)]
+    tasks, expected = _batch_case(32, shapes, fused_every=3)
+    with q4.Q4_0LinearBatch(tasks) as batch:
+        batch.launch()
+        torch.cuda.synchronize()
+    _check_batch(tasks, expected)
+
+
+def test_batch_rejects_unsupported_tasks_and_injected_allocation_failure() -> None:
+    tasks, _ = _batch_case(33, [(1, 96, 16, 0, 16)])  # K % 256 != 0
+    with pytest.raises(_lib.QxtError) as info:
+        q4.Q4_0LinearBatch(tasks)
+    assert info.value.status == _lib.INVALID_ARGUMENT
+    tasks, _ = _batch_case(34, [(1, 256, 16, 0, 16)])
+    _lib.set_failure_mask(_lib.FAIL_ALLOCATION)
+    try:
+        with pytest.raises(_lib.QxtError) as info:
+            q4.Q4_0LinearBatch(tasks)
+        assert info.value.status == _lib.ALLOCATION_FAILED
+    finally:
+        _lib.set_failure_mask(_lib.FAIL_NONE)
