@@ -19,6 +19,7 @@
 // exact integer sum does not depend on how the chunk is ordered) and receives
 // D[8 * (r / 4) + 4 * (l / 32) + r % 4][l % 32] in accumulator register r.
 #include <algorithm>
+#include <type_traits>
 
 #include "qxt_common.h"
 
@@ -26,8 +27,6 @@ namespace qxt {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int BK = 64;          // K bytes per LDS stage
-constexpr int LDS_ROW = BK + 16;  // padded row pitch in bytes
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -47,104 +46,97 @@ struct GemmArgs {
     float *y;
     size_t ldy;
     int m, n, k;
+    uint32_t a_bytes, w_bytes;  // extents of the operands (buffer-descriptor ranges)
 };
 
-template <int BM, int BN, bool K4N, int EPI>
-__global__ __launch_bounds__(kThreads) void w8a8_gemm_kernel(GemmArgs args) {
-    __shared__ __attribute__((aligned(16))) uint8_t As[BM * LDS_ROW];
-    __shared__ __attribute__((aligned(16))) uint8_t Bs[BN * LDS_ROW];
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 
-    constexpr int WM = BM / 2, WN = BN / 2;      // per-wave sub-tile
-    constexpr int TM = WM / 32, TN = WN / 32;    // 32x32 blocks per wave
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * BM;
-    const int n0 = blockIdx.x * BN;
+// Raw buffer descriptor over `bytes` bytes at `base` (gfx9 dword3: 32-bit data
+// format).  Loads at offsets >= `bytes` return zeros, which predicates the
+// matrix edges without branches.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, 0x00020000);
+}
 
-    v16i acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+constexpr uint32_t kOutOfRange = 0x80000000u;  // operands are < 2 GiB, so this offset is always out of range
 
-    for (int k0 = 0; k0 < args.k; k0 += BK) {
-        // ---- global -> LDS: A tile, 16-byte chunks (4 per row).
+// Global -> register staging of one K stage (BKT bytes of K): A rows [m0, m0+BM)
+// and B columns [n0, n0+BN) as 16-byte chunks, zeros outside the matrices.
+template <int BM, int BN, int BKT, bool K4N>
+struct StageRegs {
+    static constexpr int CPR = BKT / 16;  // chunks per LDS row
+    static constexpr int A_CHUNKS = BM * CPR / kThreads;
+    static constexpr int B_CHUNKS = BN * CPR / kThreads;
+    static constexpr int STORES = A_CHUNKS + (K4N ? 4 : 1) * B_CHUNKS;  // LDS write instructions
+    v4u a[A_CHUNKS];
+    v4u b[B_CHUNKS];
+
+    __device__ __forceinline__ void load(const GemmArgs &args, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
+                                         int m0, int n0, int k0) {
 #pragma unroll
-        for (int c = tid; c < BM * (BK / 16); c += kThreads) {
-            const int row = c >> 2, kc = c & 3;
+        for (int i = 0; i < A_CHUNKS; ++i) {
+            const int c = threadIdx.x + i * kThreads;
+            const int row = c / CPR, kc = c % CPR;
             const int gm = m0 + row, gk = k0 + kc * 16;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (gm < args.m && gk < args.k)
-                v = *reinterpret_cast<const uint4 *>(args.a + static_cast<size_t>(gm) * args.lda + gk);
-            *reinterpret_cast<uint4 *>(As + row * LDS_ROW + kc * 16) = v;
+            const uint32_t off = (gm < args.m && gk < args.k) ? static_cast<uint32_t>(gm) * args.lda + gk : kOutOfRange;
+            a[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
         }
-        // ---- global -> LDS: B tile.
-        if constexpr (!K4N) {
 #pragma unroll
-            for (int c = tid; c < BN * (BK / 16); c += kThreads) {
-                const int row = c >> 2, kc = c & 3;
+        for (int i = 0; i < B_CHUNKS; ++i) {
+            const int c = threadIdx.x + i * kThreads;
+            uint32_t off;
+            if constexpr (!K4N) {
+                const int row = c / CPR, kc = c % CPR;
                 const int gn = n0 + row, gk = k0 + kc * 16;
-                uint4 v = make_uint4(0, 0, 0, 0);
-                if (gn < args.n && gk < args.k)
-                    v = *reinterpret_cast<const uint4 *>(args.w + static_cast<size_t>(gn) * args.ldw + gk);
-                *reinterpret_cast<uint4 *>(Bs + row * LDS_ROW + kc * 16) = v;
-            }
-        } else {
-            // uint32 [K/4, N]: a 16-byte chunk holds k-quad k4 of 4 adjacent columns.
-#pragma unroll
-            for (int c = tid; c < (BK / 4) * (BN / 4); c += kThreads) {
+                off = (gn < args.n && gk < args.k) ? static_cast<uint32_t>(gn) * args.ldw + gk : kOutOfRange;
+            } else {
+                // uint32 [K/4, N]: one chunk = k-quad k4 of 4 adjacent columns.
                 const int k4 = c / (BN / 4), nq = c % (BN / 4);
                 const int gn = n0 + nq * 4, gk = k0 + k4 * 4;
-                uint4 v = make_uint4(0, 0, 0, 0);
-                if (gn < args.n && gk < args.k)
-                    v = *reinterpret_cast<const uint4 *>(args.w + static_cast<size_t>(gk / 4) * args.ldw +
-                                                         static_cast<size_t>(gn) * 4);
-                *reinterpret_cast<uint32_t *>(Bs + (nq * 4 + 0) * LDS_ROW + k4 * 4) = v.x;
-                *reinterpret_cast<uint32_t *>(Bs + (nq * 4 + 1) * LDS_ROW + k4 * 4) = v.y;
-                *reinterpret_cast<uint32_t *>(Bs + (nq * 4 + 2) * LDS_ROW + k4 * 4) = v.z;
-                *reinterpret_cast<uint32_t *>(Bs + (nq * 4 + 3) * LDS_ROW + k4 * 4) = v.w;
+                off = (gn < args.n && gk < args.k) ? static_cast<uint32_t>(gk / 4) * args.ldw + gn * 4 : kOutOfRange;
             }
+            b[i] = __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 0);
         }
-        __syncthreads();
-
-        // ---- MFMA over the 64-byte K stage (two 32-deep steps).
-#pragma unroll
-        for (int kk = 0; kk < BK; kk += 32) {
-            v4i af[TM], bf[TN];
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-                af[i] = *reinterpret_cast<const v4i *>(As + (wm * WM + i * 32 + (lane & 31)) * LDS_ROW + kk +
-                                                       (lane >> 5) * 16);
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-                bf[j] = *reinterpret_cast<const v4i *>(Bs + (wn * WN + j * 32 + (lane & 31)) * LDS_ROW + kk +
-                                                       (lane >> 5) * 16);
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-        __syncthreads();
     }
 
-    // ---- epilogue.
+    __device__ __forceinline__ void store(uint8_t *As, uint8_t *Bs) const {
+        constexpr int ROW = BKT + 16;
+#pragma unroll
+        for (int i = 0; i < A_CHUNKS; ++i) {
+            const int c = threadIdx.x + i * kThreads;
+            *reinterpret_cast<v4u *>(As + (c / CPR) * ROW + (c % CPR) * 16) = a[i];
+        }
+#pragma unroll
+        for (int i = 0; i < B_CHUNKS; ++i) {
+            const int c = threadIdx.x + i * kThreads;
+            if constexpr (!K4N) {
+                *reinterpret_cast<v4u *>(Bs + (c / CPR) * ROW + (c % CPR) * 16) = b[i];
+            } else {
+                const int k4 = c / (BN / 4), nq = c % (BN / 4);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) *reinterpret_cast<uint32_t *>(Bs + (nq * 4 + q) * ROW + k4 * 4) = b[i][q];
+            }
+        }
+    }
+};
+
+// Write one wave's TM x TN blocks of 32 x 32 accumulators (rows from mrow0,
+// columns from ncol0): int32 as is, or fl32(fl32(float(acc) * sa) * sw) (+ bias).
+template <int TM, int TN, int EPI>
+__device__ __forceinline__ void store_tile(const GemmArgs &args, const v16i (&acc)[TM][TN], int mrow0, int ncol0,
+                                           int lane) {
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            const int gn = n0 + wn * WN + j * 32 + (lane & 31);
+            const int gn = ncol0 + j * 32 + (lane & 31);
             if (gn >= args.n) continue;
             float swn = 0.0f, bn = 0.0f;
             if constexpr (EPI != EPI_I32) swn = args.sw[gn];
             if constexpr (EPI == EPI_DEQUANT_BIAS) bn = args.bias[gn];
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int gm = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                const int gm = mrow0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (gm >= args.m) continue;
                 const int v = acc[i][j][r];
                 if constexpr (EPI == EPI_I32) {
@@ -164,6 +156,256 @@ __global__ __launch_bounds__(kThreads) void w8a8_gemm_kernel(GemmArgs args) {
     }
 }
 
+// BM x BN output tile per 256-thread workgroup; waves 2 x 2, each (BM/2) x (BN/2)
+// as (BM/64) x (BN/64) blocks of 32 x 32.  K advances BKT bytes per stage
+// through two LDS buffers (rows padded by 16 bytes, so the 16-byte fragment
+// reads of 8 consecutive rows hit distinct banks): the next stage's global
+// loads are issued before the current stage's MFMAs and written to the other
+// buffer after them, one barrier per stage.  Within a stage the fragments of
+// the next 32-deep k step are read from LDS while the current step's MFMAs run.
+template <int BM, int BN, int BKT, int DEPTH, int STORE_KS, bool K4N, int EPI>
+__global__ __launch_bounds__(kThreads) void w8a8_gemm_kernel(GemmArgs args) {
+    constexpr int ROW = BKT + 16;
+    constexpr int STAGE = (BM + BN) * ROW;
+    constexpr int KSTEPS = BKT / 32;
+    static_assert(KSTEPS % 2 == 0, "fragment double buffer assumes an even number of k steps");
+    static_assert(DEPTH == 1 || DEPTH == 2, "one or two register stages in flight");
+    static_assert(STORE_KS >= 0 && STORE_KS < KSTEPS, "store step inside the stage");
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE];
+
+    constexpr int WM = BM / 2, WN = BN / 2;    // per-wave sub-tile
+    constexpr int TM = WM / 32, TN = WN / 32;  // 32x32 blocks per wave
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * BM;
+    const int n0 = blockIdx.x * BN;
+    const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(args.a, args.a_bytes);
+    const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(args.w, args.w_bytes);
+
+    v16i acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+    // Lane-constant parts of the fragment addresses.
+    const int a_lane = (wm * WM + (lane & 31)) * ROW + (lane >> 5) * 16;
+    const int b_lane = (wn * WN + (lane & 31)) * ROW + (lane >> 5) * 16;
+    v4i af[2][TM], bf[2][TN];
+    auto read_frags = [&](const uint8_t *As, const uint8_t *Bs, int kk, int buf) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) af[buf][i] = *reinterpret_cast<const v4i *>(As + a_lane + i * 32 * ROW + kk);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bf[buf][j] = *reinterpret_cast<const v4i *>(Bs + b_lane + j * 32 * ROW + kk);
+    };
+
+    // DEPTH register stages in flight.  DEPTH == 1: stage s+1 is loaded at the
+    // start of stage s and written to LDS in k step STORE_KS of stage s.
+    // DEPTH == 2: stage s+2 is loaded at the start of stage s while stage s+1
+    // (loaded a full stage earlier) is written in k step STORE_KS.
+    const int stages = (args.k + BKT - 1) / BKT;
+    StageRegs<BM, BN, BKT, K4N> regs[DEPTH];
+    regs[0].load(args, ra, rb, m0, n0, 0);
+    regs[0].store(smem, smem + BM * ROW);
+    if constexpr (DEPTH == 2) regs[1].load(args, ra, rb, m0, n0, BKT);
+    __syncthreads();
+    read_frags(smem, smem + BM * ROW, 0, 0);
+
+    // The loop body is one basic block: past the last stages the prefetch
+    // offsets are out of range (zeros, no memory traffic) and land in a
+    // buffer nobody reads again, so no branch splits the schedule.
+    auto stage_body = [&](int s, StageRegs<BM, BN, BKT, K4N> &prefetch, const StageRegs<BM, BN, BKT, K4N> &ready) {
+        const uint8_t *As = smem + (s & 1) * STAGE;
+        const uint8_t *Bs = As + BM * ROW;
+        uint8_t *next = smem + ((s + 1) & 1) * STAGE;
+        prefetch.load(args, ra, rb, m0, n0, (s + DEPTH) * BKT);
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+            // One scheduling region per k step: the TM*TN independent MFMAs of
+            // this step, the LDS reads of the next step's fragments and, in
+            // step STORE_KS, the LDS writes of stage s+1 (into the buffer no
+            // wave reads during this stage).
+            if (ks + 1 < KSTEPS) read_frags(As, Bs, (ks + 1) * 32, (ks + 1) & 1);
+            if (ks == STORE_KS) ready.store(next, next + BM * ROW);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks & 1][i], bf[ks & 1][j], acc[i][j], 0, 0, 0);
+            // Issue order inside the region: one MFMA, (first step: the global
+            // prefetch; store step: the LDS writes), the LDS reads, then the
+            // remaining MFMAs hide their latency.
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (ks == 0)
+                __builtin_amdgcn_sched_group_barrier(0x020, StageRegs<BM, BN, BKT, K4N>::A_CHUNKS +
+                                                                StageRegs<BM, BN, BKT, K4N>::B_CHUNKS, 0);
+            if (ks == STORE_KS)
+                __builtin_amdgcn_sched_group_barrier(0x200, StageRegs<BM, BN, BKT, K4N>::STORES, 0);
+            if (ks + 1 < KSTEPS) __builtin_amdgcn_sched_group_barrier(0x100, TM + TN, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - 1, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        __syncthreads();
+        read_frags(next, next + BM * ROW, 0, 0);
+    };
+    if constexpr (DEPTH == 1) {
+        for (int s = 0; s < stages; ++s) stage_body(s, regs[0], regs[0]);
+    } else {
+        int s = 0;
+        for (; s + 1 < stages; s += 2) {
+            stage_body(s, regs[0], regs[1]);
+            stage_body(s + 1, regs[1], regs[0]);
+        }
+        if (s < stages) stage_body(s, regs[0], regs[1]);
+    }
+
+    store_tile<TM, TN, EPI>(args, acc, m0 + wm * WM, n0 + wn * WN, lane);
+}
+
+// ----------------------------------------------------------------------------
+// Large-tile streaming kernel for the common case: weight layout [N, K],
+// K % 128 == 0.  256 x 256 x 128 stages, two register stages in flight, and
+// every k step of a stage issues its memory work one instruction per MFMA:
+// 8 fragment reads of the next k step, 4 LDS writes of stage s+1 (loaded a
+// full stage earlier) and 4 global loads of stage s+2 between 16 MFMAs, so
+// the single wave per SIMD never stops feeding the matrix pipe for long.
+// Rows past M or N need no predicate: their offsets fall outside the
+// buffer descriptor's range and load zeros.
+namespace big {
+constexpr int BM = 256, BN = 256, BKT = 128;
+constexpr int ROW = BKT + 16;              // LDS row pitch (bytes)
+constexpr int STAGE = (BM + BN) * ROW;     // one LDS buffer (A then B)
+constexpr int CPR = BKT / 16;              // 16-byte chunks per row
+constexpr int RPI = kThreads / CPR;        // rows covered by one load instruction
+constexpr int A_CHUNKS = BM / RPI;         // 8
+constexpr int B_CHUNKS = BN / RPI;         // 8
+constexpr int KSTEPS = BKT / 32;           // 4
+constexpr int TM = 4, TN = 4;              // 32x32 blocks per wave (128 x 128)
+constexpr int PER_STEP = (A_CHUNKS + B_CHUNKS) / KSTEPS;  // loads (and writes) per k step
+}  // namespace big
+
+template <int EPI>
+__global__ __launch_bounds__(kThreads) void w8a8_gemm_stream_kernel(GemmArgs args) {
+    using namespace big;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * BM;
+    const int n0 = blockIdx.x * BN;
+    const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(args.a, args.a_bytes);
+    const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(args.w, args.w_bytes);
+    const uint32_t lda = static_cast<uint32_t>(args.lda), ldw = static_cast<uint32_t>(args.ldw);
+
+    // This thread's chunk: row tid / CPR (+ RPI per instruction), 16 bytes at (tid % CPR) * 16.
+    const int crow = threadIdx.x / CPR, ccol = (threadIdx.x % CPR) * 16;
+    const uint32_t a_off = static_cast<uint32_t>(m0 + crow) * lda + ccol;
+    const uint32_t b_off = static_cast<uint32_t>(n0 + crow) * ldw + ccol;
+    const int st_off = crow * ROW + ccol;
+
+    v16i acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+    const int a_lane = (wm * 128 + (lane & 31)) * ROW + (lane >> 5) * 16;
+    const int b_lane = (wn * 128 + (lane & 31)) * ROW + (lane >> 5) * 16;
+    v4i af[2][TM], bf[2][TN];
+    auto read_frags = [&](const uint8_t *As, int kk, int buf) {
+        const uint8_t *Bs = As + BM * ROW;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) af[buf][i] = *reinterpret_cast<const v4i *>(As + a_lane + i * 32 * ROW + kk);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bf[buf][j] = *reinterpret_cast<const v4i *>(Bs + b_lane + j * 32 * ROW + kk);
+    };
+    // Chunk q (0 .. A_CHUNKS+B_CHUNKS-1) of a stage: A rows for q < A_CHUNKS, else B rows.
+    auto load_chunk = [&](v4u &dst, int q, int k0) {
+        if (q < A_CHUNKS)
+            dst = __builtin_amdgcn_raw_buffer_load_b128(ra, a_off + static_cast<uint32_t>(q * RPI) * lda + k0, 0, 0);
+        else
+            dst = __builtin_amdgcn_raw_buffer_load_b128(
+                rb, b_off + static_cast<uint32_t>((q - A_CHUNKS) * RPI) * ldw + k0, 0, 0);
+    };
+    auto store_chunk = [&](uint8_t *stage, const v4u &src, int q) {
+        const int row0 = q < A_CHUNKS ? q * RPI : BM + (q - A_CHUNKS) * RPI;
+        *reinterpret_cast<v4u *>(stage + st_off + row0 * ROW) = src;
+    };
+
+    constexpr int Q = A_CHUNKS + B_CHUNKS;
+    v4u regs0[Q], regs1[Q];
+    const int stages = args.k / BKT;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) load_chunk(regs0[q], q, 0);
+#pragma unroll
+    for (int q = 0; q < Q; ++q) load_chunk(regs1[q], q, BKT);
+#pragma unroll
+    for (int q = 0; q < Q; ++q) store_chunk(smem, regs0[q], q);
+    __syncthreads();
+    read_frags(smem, 0, 0);
+
+    // Stage s computes from buffer s&1, writes stage s+1 (held in `ready`) to
+    // buffer (s+1)&1 and loads stage s+2 into `prefetch` (past the end the
+    // offsets exceed the descriptor range: zeros, nothing read).
+    auto stage_body = [&](int s, v4u (&prefetch)[Q], const v4u (&ready)[Q]) {
+        const uint8_t *As = smem + (s & 1) * STAGE;
+        uint8_t *next = smem + ((s + 1) & 1) * STAGE;
+        const int k2 = (s + 2) * BKT;
+        auto kstep = [&](auto ksc) {
+            constexpr int ks = decltype(ksc)::value;
+            if constexpr (ks + 1 < KSTEPS) read_frags(As, (ks + 1) * 32, (ks + 1) & 1);
+#pragma unroll
+            for (int q = ks * PER_STEP; q < (ks + 1) * PER_STEP; ++q) store_chunk(next, ready[q], q);
+#pragma unroll
+            for (int q = ks * PER_STEP; q < (ks + 1) * PER_STEP; ++q) load_chunk(prefetch[q], q, k2);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks & 1][i], bf[ks & 1][j], acc[i][j], 0, 0, 0);
+            // One memory instruction after each MFMA: reads, then writes, then loads.
+            constexpr int reads = (ks + 1 < KSTEPS) ? TM + TN : 0;
+#pragma unroll
+            for (int t = 0; t < reads; ++t) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+#pragma unroll
+            for (int t = 0; t < PER_STEP; ++t) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+            }
+#pragma unroll
+            for (int t = 0; t < PER_STEP; ++t) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - reads - 2 * PER_STEP, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        kstep(std::integral_constant<int, 0>{});
+        kstep(std::integral_constant<int, 1>{});
+        kstep(std::integral_constant<int, 2>{});
+        kstep(std::integral_constant<int, 3>{});
+        static_assert(KSTEPS == 4, "stage body is written for four k steps");
+        __syncthreads();
+        read_frags(next, 0, 0);
+    };
+    int s = 0;
+    for (; s + 1 < stages; s += 2) {
+        stage_body(s, regs0, regs1);
+        stage_body(s + 1, regs1, regs0);
+    }
+    if (s < stages) stage_body(s, regs0, regs1);
+
+    store_tile<TM, TN, EPI>(args, acc, m0 + wm * 128, n0 + wn * 128, lane);
+}
+
 __global__ __launch_bounds__(kThreads) void dequantize_kernel(const int32_t *__restrict__ acc, size_t ldacc,
                                                               const float *__restrict__ sa,
                                                               const float *__restrict__ sw,
@@ -181,18 +423,48 @@ __global__ __launch_bounds__(kThreads) void dequantize_kernel(const int32_t *__r
     }
 }
 
-template <int BM, int BN, bool K4N>
-int launch_gemm(const GemmArgs &args, int epi, hipStream_t stream) {
+// Pipeline shape of the large-tile kernel: register stages in flight and the k
+// step of a stage that writes the next stage to LDS.
+#ifndef QXT_GEMM_DEPTH
+#define QXT_GEMM_DEPTH 1
+#endif
+#ifndef QXT_GEMM_STORE_KS
+#define QXT_GEMM_STORE_KS 2
+#endif
+
+template <int BM, int BN, int BKT, int DEPTH, int STORE_KS, bool K4N>
+int launch_gemm(GemmArgs args, int epi, uint32_t layout, hipStream_t stream) {
+    args.a_bytes = static_cast<uint32_t>(static_cast<size_t>(args.m - 1) * args.lda + args.k);
+    args.w_bytes = layout == QXT_W8A8_WEIGHT_K4N
+                       ? static_cast<uint32_t>(static_cast<size_t>(args.k / 4 - 1) * args.ldw + args.n * 4)
+                       : static_cast<uint32_t>(static_cast<size_t>(args.n - 1) * args.ldw + args.k);
     dim3 grid((args.n + BN - 1) / BN, (args.m + BM - 1) / BM, 1);
-    auto kernel = epi == EPI_I32        ? w8a8_gemm_kernel<BM, BN, K4N, EPI_I32>
-                  : epi == EPI_DEQUANT ? w8a8_gemm_kernel<BM, BN, K4N, EPI_DEQUANT>
-                                       : w8a8_gemm_kernel<BM, BN, K4N, EPI_DEQUANT_BIAS>;
+    auto kernel = epi == EPI_I32        ? w8a8_gemm_kernel<BM, BN, BKT, DEPTH, STORE_KS, K4N, EPI_I32>
+                  : epi == EPI_DEQUANT ? w8a8_gemm_kernel<BM, BN, BKT, DEPTH, STORE_KS, K4N, EPI_DEQUANT>
+                                       : w8a8_gemm_kernel<BM, BN, BKT, DEPTH, STORE_KS, K4N, EPI_DEQUANT_BIAS>;
     return launch("w8a8_gemm_kernel", kernel, grid, dim3(kThreads), 0, stream, args);
 }
 
 int run_gemm(const GemmArgs &args, int epi, uint32_t layout, hipStream_t stream) {
-    if (layout == QXT_W8A8_WEIGHT_K4N) return launch_gemm<128, 128, true>(args, epi, stream);
-    return launch_gemm<128, 128, false>(args, epi, stream);
+    // 256 x 256 tiles once they give every CU a workgroup; 128 x 128 below that.
+    const long big_tiles = static_cast<long>((args.m + 255) / 256) * ((args.n + 255) / 256);
+    const bool big = big_tiles >= compute_units();
+    constexpr int D = QXT_GEMM_DEPTH, S = QXT_GEMM_STORE_KS;
+    if (big && layout == QXT_W8A8_WEIGHT_NK && args.k % big::BKT == 0) {
+        GemmArgs a2 = args;
+        a2.a_bytes = static_cast<uint32_t>(static_cast<size_t>(args.m - 1) * args.lda + args.k);
+        a2.w_bytes = static_cast<uint32_t>(static_cast<size_t>(args.n - 1) * args.ldw + args.k);
+        dim3 grid((args.n + big::BN - 1) / big::BN, (args.m + big::BM - 1) / big::BM, 1);
+        auto kernel = epi == EPI_I32        ? w8a8_gemm_stream_kernel<EPI_I32>
+                      : epi == EPI_DEQUANT ? w8a8_gemm_stream_kernel<EPI_DEQUANT>
+                                           : w8a8_gemm_stream_kernel<EPI_DEQUANT_BIAS>;
+        return launch("w8a8_gemm_kernel", kernel, grid, dim3(kThreads), 0, stream, a2);
+    }
+    if (layout == QXT_W8A8_WEIGHT_K4N)
+        return big ? launch_gemm<256, 256, 128, D, S, true>(args, epi, layout, stream)
+                   : launch_gemm<128, 128, 64, 1, 1, true>(args, epi, layout, stream);
+    return big ? launch_gemm<256, 256, 128, D, S, false>(args, epi, layout, stream)
+               : launch_gemm<128, 128, 64, 1, 1, false>(args, epi, layout, stream);
 }
 
 int validate_gemm(const int8_t *a, size_t lda, const void *w, size_t ldw, uint32_t m, uint32_t n, uint32_t k,
@@ -212,6 +484,9 @@ int validate_gemm(const int8_t *a, size_t lda, const void *w, size_t ldw, uint32
         return fail(QXT_INVALID_ARGUMENT, "w8a8 gemm: NK weight needs 16-byte aligned rows of >= k bytes");
     if (layout == QXT_W8A8_WEIGHT_K4N && (n % 4 || ldw < static_cast<size_t>(n) * 4 || ldw % 16))
         return fail(QXT_INVALID_ARGUMENT, "w8a8 gemm: K4N weight needs n %% 4 == 0 and 16-byte aligned rows");
+    const size_t w_rows = layout == QXT_W8A8_WEIGHT_K4N ? k / 4 : n;
+    if (static_cast<size_t>(m) * lda >= (1ull << 31) || w_rows * ldw >= (1ull << 31))
+        return fail(QXT_INVALID_ARGUMENT, "w8a8 gemm: operands must be smaller than 2 GiB");
     return QXT_OK;
 }
 

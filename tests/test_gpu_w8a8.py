@@ -69,7 +69,10 @@ def test_fused_dequantize_fixture_bit_exact() -> None:
 
 @pytest.mark.parametrize(
     "m,n,k",
-    [(1, 16, 16), (7, 33, 48), (129, 257, 64), (128, 128, 4096), (300, 1000, 1040), (1, 4096, 14336), (64, 14336, 4096)],
+    [(1, 16, 16), (7, 33, 48), (129, 257, 64), (128, 128, 4096), (300, 1000, 1040), (1, 4096, 14336), (64, 14336, 4096),
+     # >= 256 tiles of 256 x 256 with K % 128 == 0: the large-tile streaming kernel,
+     # with partial edge tiles and one / two K stages.
+     (4000, 4100, 1024), (4096, 4096, 256), (4352, 4096, 128)],
 )
 def test_gemm_i32_random_shapes_exact(m: int, n: int, k: int) -> None:
     rng = np.random.default_rng(m * 7 + n * 3 + k)
@@ -77,6 +80,20 @@ def test_gemm_i32_random_shapes_exact(m: int, n: int, k: int) -> None:
     w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
     out = gemm_int8.w8a8_gemm_i32(dev(a), dev(w))
     np.testing.assert_array_equal(out.cpu().numpy(), oracle.int8_gemm_i32(a, w))
+
+
+def test_streaming_kernel_fused_epilogue_on_edge_tiles_bit_exact() -> None:
+    rng = np.random.default_rng(2718)
+    m, n, k = 4000, 4100, 512
+    a = rng.integers(-127, 128, size=(m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    sa = rng.uniform(0.001, 0.1, m).astype(np.float32)
+    sw = rng.uniform(0.001, 0.1, n).astype(np.float32)
+    bias = rng.standard_normal(n, dtype=np.float32)
+    out = gemm_int8.w8a8_gemm_dequantize(dev(a), dev(w), dev(sa), dev(sw), dev(bias)).cpu().numpy()
+    rows = np.array([0, 1, 255, 256, 3839, 3840, 3999])
+    expected = oracle.dequantize_epilogue(oracle.int8_gemm_i32(a[rows], w), sa[rows], sw, bias)
+    np.testing.assert_array_equal(out[rows], expected)
 
 
 def test_gemm_i32_extreme_accumulators_exact() -> None:
