@@ -56,7 +56,10 @@ struct Q4Task {
 struct Q4Item {
     int task;
     int col_base;
+    int ncols;  // columns of this work item (<= the task's cpw)
 };
+
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 
 // LDS geometry (in 32-bit words) for a row group of MR rows.
 struct Q4Lds {
@@ -191,36 +194,111 @@ __device__ __forceinline__ void load_units(const Q4Task &t, int col_base, int G,
         if (u < units) {
             const int col = u / G;
             const int g = u - col * G;
-            const uint4 *src = reinterpret_cast<const uint4 *>(
+            const v4u *src = reinterpret_cast<const v4u *>(
                 t.w + static_cast<size_t>(t.wcol0 + col_base + col) * t.w_stride + static_cast<size_t>(g) * 144);
 #pragma unroll
             for (int v = 0; v < 9; ++v) {
-                const uint4 x = src[v];
-                d[j][4 * v + 0] = x.x;
-                d[j][4 * v + 1] = x.y;
-                d[j][4 * v + 2] = x.z;
-                d[j][4 * v + 3] = x.w;
+                const v4u x = src[v];
+                d[j][4 * v + 0] = x[0];
+                d[j][4 * v + 1] = x[1];
+                d[j][4 * v + 2] = x[2];
+                d[j][4 * v + 3] = x[3];
             }
         }
     }
 }
 
-template <int MR, int U, bool FAST, bool DOTS, bool BATCH>
-__global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Task single, const Q4Task *__restrict__ tasks,
-                                                               const Q4Item *__restrict__ items) {
-    extern __shared__ int lds[];
-    Q4Task t;
-    int col_base, r0;
-    if constexpr (BATCH) {
-        const Q4Item item = items[blockIdx.x];
-        t = tasks[item.task];
-        col_base = item.col_base;
-        r0 = 0;
-    } else {
-        t = single;
-        col_base = blockIdx.x * t.cpw;
-        r0 = blockIdx.y * MR;
+// Phase 2 of the fast path for one round of U units per thread (units
+// first + j * kThreads + tid): the 8 block terms of every unit go to cb, or
+// (DOTS) the exact int32 block dots go to t.dots.
+template <int MR, int U, bool DOTS>
+__device__ __forceinline__ void compute_fast(const Q4Task &t, int col_base, int r0, int G, int units, int first,
+                                             const uint32_t (&wr)[U][36], const int *aq, const int *ad, float *cb,
+                                             const Q4Lds &geo) {
+    const int B = t.blocks;
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+        const int u = first + j * kThreads + threadIdx.x;
+        if (u >= units) continue;
+        const int col = u / G;
+        const int g = u - col * G;
+        float terms[MR][8];
+        int idots[MR][8];
+        auto do_block = [&](auto ic) {
+            constexpr int I = decltype(ic)::value;
+            uint32_t sbits, qs[4];
+            unit_block<I>(wr[j], sbits, qs);
+            const float dw = half_bits_to_float(sbits);
+            const int b = g * 8 + I;
+#pragma unroll
+            for (int r = 0; r < MR; ++r) {
+                const int2 ds = *reinterpret_cast<const int2 *>(ad + r * geo.ad_row + ad_index(b));
+                const int dot = block_dot(qs, aq + r * geo.aq_row + aq_index(b, 0), ds.y);
+                idots[r][I] = dot;
+                float v = static_cast<float>(dot) * dw;
+                v = v * __int_as_float(ds.x);
+                terms[r][I] = v;
+            }
+        };
+        do_block(std::integral_constant<int, 0>{});
+        do_block(std::integral_constant<int, 1>{});
+        do_block(std::integral_constant<int, 2>{});
+        do_block(std::integral_constant<int, 3>{});
+        do_block(std::integral_constant<int, 4>{});
+        do_block(std::integral_constant<int, 5>{});
+        do_block(std::integral_constant<int, 6>{});
+        do_block(std::integral_constant<int, 7>{});
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+            if constexpr (DOTS) {
+                if (r0 + r < t.rows) {
+                    int32_t *out = t.dots + (static_cast<size_t>(r0 + r) * t.ncols + col_base + col) * B + g * 8;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) out[i] = idots[r][i];
+                }
+            } else {
+                float4 *c4 = reinterpret_cast<float4 *>(cb + (r * t.cpw + col) * geo.cbs + g * 8);
+                c4[0] = make_float4(terms[r][0], terms[r][1], terms[r][2], terms[r][3]);
+                c4[1] = make_float4(terms[r][4], terms[r][5], terms[r][6], terms[r][7]);
+            }
+        }
     }
+}
+
+// Phase 3: one thread per (row, column) adds the column's block terms in
+// block order and stores the fp32 result.
+template <int MR, bool FAST>
+__device__ __forceinline__ void sum_store(const Q4Task &t, int col_base, int r0, int tile_cols, const float *cb,
+                                          const Q4Lds &geo) {
+    const int B = t.blocks;
+    for (int k = threadIdx.x; k < MR * tile_cols; k += kThreads) {
+        const int r = k / tile_cols;
+        const int col = k - r * tile_cols;
+        if (r0 + r >= t.rows) continue;
+        const float *c = cb + (r * t.cpw + col) * geo.cbs;
+        float acc = 0.0f;
+        if constexpr (FAST) {
+            for (int b = 0; b < B; b += 4) {
+                const float4 v = *reinterpret_cast<const float4 *>(c + b);
+                acc += v.x;
+                acc += v.y;
+                acc += v.z;
+                acc += v.w;
+            }
+        } else {
+            for (int b = 0; b < B; ++b) acc += c[b];
+        }
+        float *out = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(t.y) + (r0 + r) * t.y_stride);
+        out[t.ocol0 + col_base + col] = acc;
+    }
+}
+
+// One linear: workgroup (x, y) owns columns [x * cpw, +cpw) and rows [y * MR, +MR).
+template <int MR, int U, bool FAST, bool DOTS>
+__global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Task t) {
+    extern __shared__ int lds[];
+    const int col_base = blockIdx.x * t.cpw;
+    const int r0 = blockIdx.y * MR;
     const int B = t.blocks;
     const Q4Lds geo(B, FAST);
     int *aq = lds;                                                 // [MR][aq_row]
@@ -239,54 +317,7 @@ __global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Task single, co
     if constexpr (FAST) {
         for (int first = 0; first < units; first += U * kThreads) {
             if (first > 0) load_units<U>(t, col_base, G, units, first, wr);
-#pragma unroll
-            for (int j = 0; j < U; ++j) {
-                const int u = first + j * kThreads + threadIdx.x;
-                if (u >= units) continue;
-                const int col = u / G;
-                const int g = u - col * G;
-                float terms[MR][8];
-                int idots[MR][8];
-                auto do_block = [&](auto ic) {
-                    constexpr int I = decltype(ic)::value;
-                    uint32_t sbits, qs[4];
-                    unit_block<I>(wr[j], sbits, qs);
-                    const float dw = half_bits_to_float(sbits);
-                    const int b = g * 8 + I;
-#pragma unroll
-                    for (int r = 0; r < MR; ++r) {
-                        const int2 ds = *reinterpret_cast<const int2 *>(ad + r * geo.ad_row + ad_index(b));
-                        const int dot = block_dot(qs, aq + r * geo.aq_row + aq_index(b, 0), ds.y);
-                        idots[r][I] = dot;
-                        float v = static_cast<float>(dot) * dw;
-                        v = v * __int_as_float(ds.x);
-                        terms[r][I] = v;
-                    }
-                };
-                do_block(std::integral_constant<int, 0>{});
-                do_block(std::integral_constant<int, 1>{});
-                do_block(std::integral_constant<int, 2>{});
-                do_block(std::integral_constant<int, 3>{});
-                do_block(std::integral_constant<int, 4>{});
-                do_block(std::integral_constant<int, 5>{});
-                do_block(std::integral_constant<int, 6>{});
-                do_block(std::integral_constant<int, 7>{});
-#pragma unroll
-                for (int r = 0; r < MR; ++r) {
-                    if constexpr (DOTS) {
-                        if (r0 + r < t.rows) {
-                            int32_t *out =
-                                t.dots + (static_cast<size_t>(r0 + r) * t.ncols + col_base + col) * B + g * 8;
-#pragma unroll
-                            for (int i = 0; i < 8; ++i) out[i] = idots[r][i];
-                        }
-                    } else {
-                        float4 *c4 = reinterpret_cast<float4 *>(cb + (r * t.cpw + col) * geo.cbs + g * 8);
-                        c4[0] = make_float4(terms[r][0], terms[r][1], terms[r][2], terms[r][3]);
-                        c4[1] = make_float4(terms[r][4], terms[r][5], terms[r][6], terms[r][7]);
-                    }
-                }
-            }
+            compute_fast<MR, U, DOTS>(t, col_base, r0, G, units, first, wr, aq, ad, cb, geo);
         }
     } else {
         for (int u = threadIdx.x; u < units; u += kThreads) {
@@ -316,42 +347,50 @@ __global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Task single, co
     }
     if constexpr (DOTS) return;
     __syncthreads();
-
-    // ---- phase 3: in-order fp32 sum per (row, column).
-    for (int k = threadIdx.x; k < MR * tile_cols; k += kThreads) {
-        const int r = k / tile_cols;
-        const int col = k - r * tile_cols;
-        if (r0 + r >= t.rows) continue;
-        const float *c = cb + (r * t.cpw + col) * geo.cbs;
-        float acc = 0.0f;
-        if constexpr (FAST) {
-            for (int b = 0; b < B; b += 4) {
-                const float4 v = *reinterpret_cast<const float4 *>(c + b);
-                acc += v.x;
-                acc += v.y;
-                acc += v.z;
-                acc += v.w;
-            }
-        } else {
-            for (int b = 0; b < B; ++b) acc += c[b];
-        }
-        float *out = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(t.y) + (r0 + r) * t.y_stride);
-        out[t.ocol0 + col_base + col] = acc;
-    }
+    sum_store<MR, FAST>(t, col_base, r0, tile_cols, cb, geo);
 }
 
-// Units each thread owns per round on the fast path (more bytes in flight at M = 1).
+// A batch of linears (fast path, rows <= MR): one workgroup per work item
+// (a column tile of one task, at most U * kThreads units), items in task
+// order.  The hardware dispatcher starts the next item's workgroup the
+// moment a slot frees.  (Measured on MI355X at the 154-linear decode step:
+// 101 us per launch this way, 138 us with a persistent grid walking the
+// item queue round-robin with one item of weight prefetch.)
+template <int MR, int U>
+__global__ __launch_bounds__(kThreads) void q4_0_batch_kernel(const Q4Task *__restrict__ tasks,
+                                                              const Q4Item *__restrict__ items) {
+    extern __shared__ int lds[];
+    const Q4Item item = items[blockIdx.x];
+    const Q4Task &t = tasks[item.task];
+    const int B = t.blocks;
+    const int G = B >> 3;
+    const int units = item.ncols * G;
+    uint32_t wr[U][36];
+    load_units<U>(t, item.col_base, G, units, 0, wr);
+    const Q4Lds geo(B, true);
+    int *aq = lds;
+    int *ad = aq + MR * geo.aq_row;
+    float *cb = reinterpret_cast<float *>(ad + MR * geo.ad_row);
+    stage_activation<MR>(t, 0, aq, ad, geo);
+    __syncthreads();
+    compute_fast<MR, U, false>(t, item.col_base, 0, G, units, 0, wr, aq, ad, cb, geo);
+    __syncthreads();
+    sum_store<MR, true>(t, item.col_base, 0, item.ncols, cb, geo);
+}
+
+// Units each thread owns per round on the fast path.
 constexpr int units_per_thread(int mr) { return mr == 1 ? 2 : 1; }
 
 bool fast_path(const Q4Task &t) { return t.blocks % 8 == 0 && aligned(t.w, 16) && t.w_stride % 16 == 0; }
 
-// Columns per workgroup and dynamic LDS bytes for a task, or an error status.
-int plan_task(Q4Task &t, int mr, bool fast, bool dots, size_t *lds) {
+// Columns per workgroup (at most `max_cpw`) and dynamic LDS bytes for a task,
+// or an error status.
+int plan_task(Q4Task &t, int mr, bool fast, bool dots, size_t *lds, int max_cpw = 1 << 30) {
     const Q4Lds geo(t.blocks, fast);
     const int units_per_col = fast ? t.blocks / 8 : t.blocks;
     const int per_round = kThreads * (fast ? units_per_thread(mr) : 1);
     int cpw = units_per_col >= per_round ? 1 : per_round / units_per_col;
-    cpw = std::max(1, std::min(cpw, t.ncols));
+    cpw = std::max(1, std::min({cpw, t.ncols, max_cpw}));
     while (cpw > 1 && geo.words(mr, dots ? 0 : cpw) * 4 > kMaxLds) --cpw;
     *lds = geo.words(mr, dots ? 0 : cpw) * 4;
     if (*lds > kMaxLds)
@@ -364,19 +403,19 @@ int plan_task(Q4Task &t, int mr, bool fast, bool dots, size_t *lds) {
 template <int MR, bool DOTS>
 int launch_single(Q4Task t, hipStream_t stream) {
     const bool fast = fast_path(t);
+    // A single linear is latency-bound unless its grid covers the chip: cap
+    // the tile width so that there are at least two workgroups per CU.
+    const int row_groups = (t.rows + MR - 1) / MR;
+    const long want = 2L * compute_units();
+    const int max_cpw = static_cast<int>(std::max<long>(1, (static_cast<long>(t.ncols) * row_groups + want - 1) / want));
     size_t lds = 0;
-    int rc = plan_task(t, MR, fast, DOTS, &lds);
+    int rc = plan_task(t, MR, fast, DOTS, &lds, max_cpw);
     if (rc != QXT_OK) return rc;
-    dim3 grid((t.ncols + t.cpw - 1) / t.cpw, (t.rows + MR - 1) / MR, 1);
+    dim3 grid((t.ncols + t.cpw - 1) / t.cpw, row_groups, 1);
     constexpr int U = units_per_thread(MR);
     const char *name = DOTS ? "q4_0_block_dots_kernel" : "q4_0_linear_kernel";
-    const Q4Task *no_tasks = nullptr;
-    const Q4Item *no_items = nullptr;
-    if (fast)
-        return launch(name, q4_0_linear_kernel<MR, U, true, DOTS, false>, grid, dim3(kThreads), lds, stream, t,
-                      no_tasks, no_items);
-    return launch(name, q4_0_linear_kernel<MR, 1, false, DOTS, false>, grid, dim3(kThreads), lds, stream, t, no_tasks,
-                  no_items);
+    if (fast) return launch(name, q4_0_linear_kernel<MR, U, true, DOTS>, grid, dim3(kThreads), lds, stream, t);
+    return launch(name, q4_0_linear_kernel<MR, 1, false, DOTS>, grid, dim3(kThreads), lds, stream, t);
 }
 
 template <bool DOTS>
@@ -414,9 +453,22 @@ struct qxt_q4_0_batch {
     const Q4Item *items = nullptr;
     uint32_t task_count = 0;
     uint32_t item_count = 0;
+    uint32_t grid = 0;
     int mr = 1;
     size_t lds = 0;
 };
+
+namespace qxt {
+namespace {
+
+using BatchKernel = void (*)(const Q4Task *, const Q4Item *);
+
+BatchKernel batch_kernel(int mr) {
+    return mr == 1 ? q4_0_batch_kernel<1, units_per_thread(1)> : q4_0_batch_kernel<4, units_per_thread(4)>;
+}
+
+}  // namespace
+}  // namespace qxt
 
 extern "C" {
 
@@ -488,6 +540,9 @@ int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_
         int rc = validate_q4(act, act_stride, d.weight, d.weight_row_stride, d.rows, d.blocks, d.column_count);
         if (rc != QXT_OK) return rc;
         if (d.rows > 4) return fail(QXT_INVALID_ARGUMENT, "q4_0 batch task %u: at most 4 rows per task", i);
+        if (d.blocks / 8 > static_cast<uint32_t>(units_per_thread(4) * kThreads))
+            return fail(QXT_INVALID_ARGUMENT, "q4_0 batch task %u: K = %u exceeds the batch limit of %d", i,
+                        d.blocks * 32, units_per_thread(4) * kThreads * 256);
         if (d.x != nullptr && (!aligned(d.x, 16) || d.x_row_stride % 16 ||
                                d.x_row_stride < static_cast<size_t>(d.blocks) * QK * sizeof(float)))
             return fail(QXT_INVALID_ARGUMENT, "q4_0 batch task %u: fp32 activation rows must be 16-byte aligned", i);
@@ -525,7 +580,8 @@ int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_
         int rc = plan_task(host[i], mr, true, false, &task_lds);
         if (rc != QXT_OK) return rc;
         lds = std::max(lds, task_lds);
-        for (int c = 0; c < host[i].ncols; c += host[i].cpw) items.push_back({static_cast<int>(i), c});
+        for (int c = 0; c < host[i].ncols; c += host[i].cpw)
+            items.push_back({static_cast<int>(i), c, std::min(host[i].cpw, host[i].ncols - c)});
     }
     if (items.size() > 0x7FFFFFFFu) return fail(QXT_INVALID_ARGUMENT, "q4_0 batch: too many work items");
     int rc = injected(QXT_FAIL_ALLOCATION);
@@ -550,6 +606,7 @@ int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_
     batch->items = reinterpret_cast<const Q4Item *>(base + task_bytes);
     batch->task_count = count;
     batch->item_count = static_cast<uint32_t>(items.size());
+    batch->grid = static_cast<uint32_t>(items.size());
     batch->mr = mr;
     batch->lds = lds;
     *out = batch;
@@ -560,13 +617,8 @@ int qxt_q4_0_batch_launch(const qxt_q4_0_batch *batch, void *stream) {
     if (batch == nullptr) return fail(QXT_INVALID_ARGUMENT, "q4_0 batch: null handle");
     int rc = injected(QXT_FAIL_SUBMISSION);
     if (rc != QXT_OK) return rc;
-    const dim3 grid(batch->item_count, 1, 1);
-    const Q4Task none{};
-    if (batch->mr == 1)
-        return launch("q4_0_batch_kernel", q4_0_linear_kernel<1, units_per_thread(1), true, false, true>, grid,
-                      dim3(kThreads), batch->lds, as_stream(stream), none, batch->tasks, batch->items);
-    return launch("q4_0_batch_kernel", q4_0_linear_kernel<4, units_per_thread(4), true, false, true>, grid,
-                  dim3(kThreads), batch->lds, as_stream(stream), none, batch->tasks, batch->items);
+    return launch("q4_0_batch_kernel", batch_kernel(batch->mr), dim3(batch->grid), dim3(kThreads), batch->lds,
+                  as_stream(stream), batch->tasks, batch->items);
 }
 
 uint32_t qxt_q4_0_batch_work_items(const qxt_q4_0_batch *batch) { return batch == nullptr ? 0 : batch->item_count; }

@@ -120,40 +120,179 @@ struct StageRegs {
     }
 };
 
+// Copy the row scales sa[m0, m0+BM), column scales sw[n0, n0+BN) and bias of
+// a workgroup's output tile into LDS (zeros past M / N).  Reading them from
+// LDS in the epilogue keeps vector-memory loads out of the run of output
+// stores (a load issued after a store would wait for that store).  The
+// caller has finished with the LDS operand tiles.
+template <int BM, int BN, int EPI>
+__device__ __forceinline__ void stage_scales(const GemmArgs &args, float *lds, int m0, int n0) {
+    if constexpr (EPI == EPI_I32) return;
+    static_assert(BM <= kThreads && BN <= kThreads, "one scale per thread");
+    const int t = threadIdx.x;
+    if (t < BM) {
+        const __amdgpu_buffer_rsrc_t rsa = buffer_rsrc(args.sa, static_cast<uint32_t>(args.m) * 4);
+        lds[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                               rsa, m0 + t < args.m ? (m0 + t) * 4 : kOutOfRange, 0, 0));
+    }
+    if (t < BN) {
+        const uint32_t off = n0 + t < args.n ? (n0 + t) * 4 : kOutOfRange;
+        const __amdgpu_buffer_rsrc_t rsw = buffer_rsrc(args.sw, static_cast<uint32_t>(args.n) * 4);
+        lds[BM + t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsw, off, 0, 0));
+        float bv = 0.0f;
+        if constexpr (EPI == EPI_DEQUANT_BIAS) {
+            const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(args.bias, static_cast<uint32_t>(args.n) * 4);
+            bv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, off, 0, 0));
+        }
+        lds[BM + BN + t] = bv;
+    }
+    __syncthreads();
+}
+
 // Write one wave's TM x TN blocks of 32 x 32 accumulators (rows from mrow0,
-// columns from ncol0): int32 as is, or fl32(fl32(float(acc) * sa) * sw) (+ bias).
-template <int TM, int TN, int EPI>
+// columns from ncol0, i.e. tile-local rows lm0 / columns ln0): int32 as is, or
+// fl32(fl32(float(acc) * sa) * sw) (+ bias) with the scales staged in LDS by
+// stage_scales.  Stores go through a buffer descriptor over the output: rows
+// past M are addressed out of its range and dropped; columns past N are
+// masked per block column.
+template <int BM, int BN, int TM, int TN, int EPI>
 __device__ __forceinline__ void store_tile(const GemmArgs &args, const v16i (&acc)[TM][TN], int mrow0, int ncol0,
-                                           int lane) {
+                                           int lm0, int ln0, int lane, const float *lds) {
+    const int half = lane >> 5;
+    void *base = EPI == EPI_I32 ? static_cast<void *>(args.acc) : static_cast<void *>(args.y);
+    const uint32_t ld = static_cast<uint32_t>(EPI == EPI_I32 ? args.ldacc : args.ldy);
+    const __amdgpu_buffer_rsrc_t ro =
+        buffer_rsrc(base, static_cast<uint32_t>(args.m - 1) * ld + static_cast<uint32_t>(args.n) * 4);
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
+    for (int j = 0; j < TN; ++j) {
+        const int gn = ncol0 + j * 32 + (lane & 31);
+        if (gn >= args.n) continue;
+        float swn = 0.0f, bn = 0.0f;
+        if constexpr (EPI != EPI_I32) {
+            swn = lds[BM + ln0 + j * 32 + (lane & 31)];
+            bn = lds[BM + BN + ln0 + j * 32 + (lane & 31)];
+        }
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int gn = ncol0 + j * 32 + (lane & 31);
-            if (gn >= args.n) continue;
-            float swn = 0.0f, bn = 0.0f;
-            if constexpr (EPI != EPI_I32) swn = args.sw[gn];
-            if constexpr (EPI == EPI_DEQUANT_BIAS) bn = args.bias[gn];
+        for (int i = 0; i < TM; ++i) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int gm = mrow0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (gm >= args.m) continue;
-                const int v = acc[i][j][r];
-                if constexpr (EPI == EPI_I32) {
-                    int32_t *out = reinterpret_cast<int32_t *>(reinterpret_cast<uint8_t *>(args.acc) +
-                                                               static_cast<size_t>(gm) * args.ldacc);
-                    out[gn] = v;
-                } else {
-                    float yv = static_cast<float>(v) * args.sa[gm];
-                    yv = yv * swn;
-                    if constexpr (EPI == EPI_DEQUANT_BIAS) yv = yv + bn;
-                    float *out = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(args.y) +
-                                                           static_cast<size_t>(gm) * args.ldy);
-                    out[gn] = yv;
+            for (int q = 0; q < 4; ++q) {
+                float4 sa4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if constexpr (EPI != EPI_I32)
+                    sa4 = *reinterpret_cast<const float4 *>(lds + lm0 + i * 32 + 8 * q + 4 * half);
+                const float sar[4] = {sa4.x, sa4.y, sa4.z, sa4.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = 4 * q + e;
+                    const int gm = mrow0 + i * 32 + 8 * q + 4 * half + e;
+                    const uint32_t off = gm < args.m ? static_cast<uint32_t>(gm) * ld + gn * 4 : kOutOfRange;
+                    const int v = acc[i][j][r];
+                    if constexpr (EPI == EPI_I32) {
+                        __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(v), ro, off, 0, 0);
+                    } else {
+                        float yv = static_cast<float>(v) * sar[e];
+                        yv = yv * swn;
+                        if constexpr (EPI == EPI_DEQUANT_BIAS) yv = yv + bn;
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, yv), ro, off, 0, 0);
+                    }
                 }
             }
         }
     }
+}
+
+// Epilogue of a 256 x 256 tile held by four waves of 128 x 128 (waves 2 x 2),
+// staged through LDS so that global stores are whole 1 KB tile rows (16
+// bytes per lane) instead of 128-byte row pieces.  Two passes: in pass p
+// every wave writes its 32-row blocks i = 2p, 2p + 1 (tile rows
+// wm * 128 + 64p + [0, 64)) to `buf` row-major, then each wave stores 32 of
+// the 128 buffered rows.  Each accumulator is converted in exactly one pass.
+// Rows past M are skipped and columns past N masked (edge lanes and
+// unaligned outputs store element by element).  `scales` holds what
+// stage_scales wrote; `buf` takes 128 KB.
+template <int EPI>
+__device__ __forceinline__ void store_tile_rows(const GemmArgs &args, const v16i (&acc)[4][4], int m0, int n0,
+                                                int wm, int wn, int lane, uint8_t *buf, const float *scales) {
+    constexpr int BM = 256, BN = 256;
+    const int hl = lane >> 5;
+    const int wave = threadIdx.x >> 6;
+    float *fb = reinterpret_cast<float *>(buf);
+    uint8_t *base = reinterpret_cast<uint8_t *>(EPI == EPI_I32 ? static_cast<void *>(args.acc)
+                                                               : static_cast<void *>(args.y));
+    const size_t ld = EPI == EPI_I32 ? args.ldacc : args.ldy;
+    const int col0 = n0 + lane * 4;
+    const bool vec = col0 + 3 < args.n && (((reinterpret_cast<uintptr_t>(base) | ld) & 15) == 0);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int col = wn * 128 + j * 32 + (lane & 31);
+            float swn = 0.0f, bn = 0.0f;
+            if constexpr (EPI != EPI_I32) {
+                swn = scales[BM + col];
+                bn = scales[BM + BN + col];
+            }
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii) {
+                const int i = 2 * p + ii;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int lr = 8 * q + 4 * hl;
+                    float4 sa4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    if constexpr (EPI != EPI_I32)
+                        sa4 = *reinterpret_cast<const float4 *>(scales + wm * 128 + i * 32 + lr);
+                    const float sar[4] = {sa4.x, sa4.y, sa4.z, sa4.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int v = acc[i][j][4 * q + e];
+                        float out;
+                        if constexpr (EPI == EPI_I32) {
+                            out = __int_as_float(v);
+                        } else {
+                            out = static_cast<float>(v) * sar[e];
+                            out = out * swn;
+                            if constexpr (EPI == EPI_DEQUANT_BIAS) out = out + bn;
+                        }
+                        fb[(wm * 64 + ii * 32 + lr + e) * BN + col] = out;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        // Lane l stores columns n0 + 4l .. 4l + 3 of each row: one 16-byte store
+        // when all four are inside N and the address is 16-byte aligned,
+        // otherwise element by element.
+#pragma unroll 4
+        for (int t = 0; t < 32; ++t) {
+            const int br = wave * 32 + t;
+            const int gm = m0 + (br >> 6) * 128 + p * 64 + (br & 63);
+            if (gm < args.m) {
+                const v4u v = *reinterpret_cast<const v4u *>(fb + br * BN + lane * 4);
+                uint8_t *dst = base + static_cast<size_t>(gm) * ld + static_cast<size_t>(col0) * 4;
+                if (vec) {
+                    *reinterpret_cast<v4u *>(dst) = v;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (col0 + e < args.n) reinterpret_cast<uint32_t *>(dst)[e] = v[e];
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// LDS bytes the 256 x 256 epilogue uses: the 128 KB half-tile buffer and
+// the staged scales behind it.
+constexpr int kEpilogueLds = 128 * 1024 + 3 * 256 * 4;
+
+// Epilogue of the 256 x 256 kernels (LDS free, all waves past their last
+// LDS read).
+template <int EPI>
+__device__ __forceinline__ void epilogue_256(const GemmArgs &args, const v16i (&acc)[4][4], int m0, int n0, int wm,
+                                             int wn, int lane, uint8_t *smem) {
+    float *scales = reinterpret_cast<float *>(smem + 128 * 1024);
+    stage_scales<256, 256, EPI>(args, scales, m0, n0);
+    store_tile_rows<EPI>(args, acc, m0, n0, wm, wn, lane, smem, scales);
 }
 
 // BM x BN output tile per 256-thread workgroup; waves 2 x 2, each (BM/2) x (BN/2)
@@ -262,7 +401,10 @@ __global__ __launch_bounds__(kThreads) void w8a8_gemm_kernel(GemmArgs args) {
         if (s < stages) stage_body(s, regs[0], regs[1]);
     }
 
-    store_tile<TM, TN, EPI>(args, acc, m0 + wm * WM, n0 + wn * WN, lane);
+    __syncthreads();
+    stage_scales<BM, BN, EPI>(args, reinterpret_cast<float *>(smem), m0, n0);
+    store_tile<BM, BN, TM, TN, EPI>(args, acc, m0 + wm * WM, n0 + wn * WN, wm * WM, wn * WN, lane,
+                                    reinterpret_cast<const float *>(smem));
 }
 
 // ----------------------------------------------------------------------------
@@ -273,7 +415,17 @@ __global__ __launch_bounds__(kThreads) void w8a8_gemm_kernel(GemmArgs args) {
 // full stage earlier) and 4 global loads of stage s+2 between 16 MFMAs, so
 // the single wave per SIMD never stops feeding the matrix pipe for long.
 // Rows past M or N need no predicate: their offsets fall outside the
-// buffer descriptor's range and load zeros.
+// buffer descriptor's range and load zeros.  Output tiles are mapped to
+// workgroups XCD by XCD (xcd_tile) and written through LDS one tile row per
+// store (store_tile_rows).
+//
+// Measured alternatives on MI355X (cfg4 shapes, realistic operand values):
+// the same tiling with operands loaded by LDS DMA (buffer_load ... lds, a
+// four-stage ring of 64-byte K stages, XOR-swizzled rows) was no faster
+// (within +-5 %), and no buffer-load cache policy changed the main loop by
+// more than noise; skipping the global loads altogether (a timing-only
+// variant) speeds the main loop up by ~1.4x, so L2 -> CU operand traffic, not
+// instruction issue, bounds it.
 namespace big {
 constexpr int BM = 256, BN = 256, BKT = 128;
 constexpr int ROW = BKT + 16;              // LDS row pitch (bytes)
@@ -285,7 +437,28 @@ constexpr int B_CHUNKS = BN / RPI;         // 8
 constexpr int KSTEPS = BKT / 32;           // 4
 constexpr int TM = 4, TN = 4;              // 32x32 blocks per wave (128 x 128)
 constexpr int PER_STEP = (A_CHUNKS + B_CHUNKS) / KSTEPS;  // loads (and writes) per k step
+static_assert(2 * STAGE >= kEpilogueLds, "the epilogue reuses the operand buffers");
 }  // namespace big
+
+// Output tile (ty, tx) of workgroup `pid` in a tm x tn tile grid.  The
+// dispatcher hands workgroups to the 8 XCDs round-robin (pid % 8), each XCD
+// with its own L2.  Every XCD is given a contiguous run of a grouped tile
+// order (GM tile rows at a time, column by column), so the workgroups one
+// XCD runs together form a compact block whose A and B panels are shared
+// through that XCD's L2 instead of being fetched by every XCD.
+constexpr int kXcds = 8;
+__device__ __forceinline__ void xcd_tile(int pid, int tm, int tn, int gm, int &ty, int &tx) {
+    const int total = tm * tn;
+    const int per = total / kXcds, rem = total % kXcds;
+    const int xcd = pid % kXcds, local = pid / kXcds;
+    const int seq = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+    const int group = seq / (gm * tn);
+    const int first = group * gm;
+    const int rows = min(gm, tm - first);
+    const int in_group = seq - group * gm * tn;
+    ty = first + in_group % rows;
+    tx = in_group / rows;
+}
 
 template <int EPI>
 __global__ __launch_bounds__(kThreads) void w8a8_gemm_stream_kernel(GemmArgs args) {
@@ -294,8 +467,10 @@ __global__ __launch_bounds__(kThreads) void w8a8_gemm_stream_kernel(GemmArgs arg
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * BM;
-    const int n0 = blockIdx.x * BN;
+    int ty, tx;
+    xcd_tile(blockIdx.x, (args.m + BM - 1) / BM, (args.n + BN - 1) / BN, 4, ty, tx);
+    const int m0 = ty * BM;
+    const int n0 = tx * BN;
     const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(args.a, args.a_bytes);
     const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(args.w, args.w_bytes);
     const uint32_t lda = static_cast<uint32_t>(args.lda), ldw = static_cast<uint32_t>(args.ldw);
@@ -403,7 +578,8 @@ __global__ __launch_bounds__(kThreads) void w8a8_gemm_stream_kernel(GemmArgs arg
     }
     if (s < stages) stage_body(s, regs0, regs1);
 
-    store_tile<TM, TN, EPI>(args, acc, m0 + wm * 128, n0 + wn * 128, lane);
+    __syncthreads();
+    epilogue_256<EPI>(args, acc, m0, n0, wm, wn, lane, smem);
 }
 
 __global__ __launch_bounds__(kThreads) void dequantize_kernel(const int32_t *__restrict__ acc, size_t ldacc,
@@ -445,20 +621,29 @@ int launch_gemm(GemmArgs args, int epi, uint32_t layout, hipStream_t stream) {
     return launch("w8a8_gemm_kernel", kernel, grid, dim3(kThreads), 0, stream, args);
 }
 
+int launch_stream(const GemmArgs &args, int epi, hipStream_t stream) {
+    GemmArgs a2 = args;
+    a2.a_bytes = static_cast<uint32_t>(static_cast<size_t>(args.m - 1) * args.lda + args.k);
+    a2.w_bytes = static_cast<uint32_t>(static_cast<size_t>(args.n - 1) * args.ldw + args.k);
+    dim3 grid(((args.n + big::BN - 1) / big::BN) * ((args.m + big::BM - 1) / big::BM), 1, 1);
+    auto kernel = epi == EPI_I32        ? w8a8_gemm_stream_kernel<EPI_I32>
+                  : epi == EPI_DEQUANT ? w8a8_gemm_stream_kernel<EPI_DEQUANT>
+                                       : w8a8_gemm_stream_kernel<EPI_DEQUANT_BIAS>;
+    return launch("w8a8_gemm_kernel", kernel, grid, dim3(kThreads), 0, stream, a2);
+}
+
 int run_gemm(const GemmArgs &args, int epi, uint32_t layout, hipStream_t stream) {
     // 256 x 256 tiles once they give every CU a workgroup; 128 x 128 below that.
-    const long big_tiles = static_cast<long>((args.m + 255) / 256) * ((args.n + 255) / 256);
-    const bool big = big_tiles >= compute_units();
+    const long cus = compute_units();
+    const long tm = (args.m + 255) / 256, tn = (args.n + 255) / 256;
+    const bool big = tm * tn >= cus;
     constexpr int D = QXT_GEMM_DEPTH, S = QXT_GEMM_STORE_KS;
     if (big && layout == QXT_W8A8_WEIGHT_NK && args.k % big::BKT == 0) {
-        GemmArgs a2 = args;
-        a2.a_bytes = static_cast<uint32_t>(static_cast<size_t>(args.m - 1) * args.lda + args.k);
-        a2.w_bytes = static_cast<uint32_t>(static_cast<size_t>(args.n - 1) * args.ldw + args.k);
-        dim3 grid((args.n + big::BN - 1) / big::BN, (args.m + big::BM - 1) / big::BM, 1);
-        auto kernel = epi == EPI_I32        ? w8a8_gemm_stream_kernel<EPI_I32>
-                      : epi == EPI_DEQUANT ? w8a8_gemm_stream_kernel<EPI_DEQUANT>
-                                           : w8a8_gemm_stream_kernel<EPI_DEQUANT_BIAS>;
-        return launch("w8a8_gemm_kernel", kernel, grid, dim3(kThreads), 0, stream, a2);
+        // (Running the last, half-empty round of 16 x 56 tiles as a second
+        // launch of 256 x 128 tiles was measured at no gain on MI355X: the
+        // generic kernel needs as long for a half tile as this one for a
+        // full tile.)
+        return launch_stream(args, epi, stream);
     }
     if (layout == QXT_W8A8_WEIGHT_K4N)
         return big ? launch_gemm<256, 256, 128, D, S, true>(args, epi, layout, stream)
@@ -513,6 +698,8 @@ int qxt_w8a8_gemm_i32(const int8_t *a, size_t lda, const void *w, size_t ldw, in
     if (rc != QXT_OK) return rc;
     if (acc == nullptr || !aligned(acc, 4) || ldacc % 4 || ldacc < static_cast<size_t>(n) * 4)
         return fail(QXT_INVALID_ARGUMENT, "w8a8 gemm: bad accumulator output");
+    if (static_cast<uint64_t>(m) * ldacc >= (1ull << 31))
+        return fail(QXT_INVALID_ARGUMENT, "w8a8 gemm: the output must be smaller than 2 GiB");
     rc = injected(QXT_FAIL_SUBMISSION);
     if (rc != QXT_OK) return rc;
     GemmArgs args{a, lda, static_cast<const uint8_t *>(w), ldw, acc, ldacc, nullptr, nullptr, nullptr,
@@ -527,6 +714,8 @@ int qxt_w8a8_gemm_dequantize(const int8_t *a, size_t lda, const void *w, size_t 
     if (rc != QXT_OK) return rc;
     rc = validate_epilogue(row_scales, column_scales, bias, y, ldy, n);
     if (rc != QXT_OK) return rc;
+    if (static_cast<uint64_t>(m) * ldy >= (1ull << 31))
+        return fail(QXT_INVALID_ARGUMENT, "w8a8 gemm: the output must be smaller than 2 GiB");
     rc = injected(QXT_FAIL_SUBMISSION);
     if (rc != QXT_OK) return rc;
     GemmArgs args{a, lda, static_cast<const uint8_t *>(w), ldw, nullptr, 0, row_scales, column_scales, bias,
@@ -556,6 +745,8 @@ int qxt_w8a8_linear(const float *x, size_t ldx, int8_t *qa, size_t ldqa, float *
     if (rc != QXT_OK) return rc;
     rc = validate_epilogue(sa, column_scales, bias, y, ldy, n);
     if (rc != QXT_OK) return rc;
+    if (static_cast<uint64_t>(m) * ldy >= (1ull << 31))
+        return fail(QXT_INVALID_ARGUMENT, "w8a8 linear: the output must be smaller than 2 GiB");
     if (x == nullptr || ldx % 4 || ldx < static_cast<size_t>(k) * 4 || !aligned(x, 4))
         return fail(QXT_INVALID_ARGUMENT, "w8a8 linear: bad activation input");
     if (flags & ~QXT_QUANT_NO_SCALE_FLOOR) return fail(QXT_INVALID_ARGUMENT, "w8a8 linear: unknown flags");

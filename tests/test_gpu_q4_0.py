@@ -212,6 +212,33 @@ def test_batch_m1_mixed_shapes_bit_exact() -> None:
         _check_batch(tasks, expected)
 
 
+def test_batch_many_work_items_eager_and_graph_replays() -> None:
+    # More column tiles than the device holds workgroups at once (several
+    # dispatch rounds), launched repeatedly, eagerly and from a captured graph.
+    shapes = [(1, 2048, 5632, 0, 5632)] * 6 + [(1, 5632, 2048, 0, 2048)] * 6 + [(1, 2048, 256, 16, 240)] * 4
+    tasks, expected = _batch_case(35, shapes)
+    with q4.Q4_0LinearBatch(tasks) as batch:
+        assert batch.work_items > 1024
+        stream = torch.cuda.Stream()
+        for _ in range(3):
+            for t in tasks:
+                t["destination"][:, 16:] = -1.0
+            batch.launch(stream)
+            stream.synchronize()
+            _check_batch(tasks, expected)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            batch.launch(stream)
+        for _ in range(3):
+            for t in tasks:
+                t["destination"][:, 16:] = -1.0
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            _check_batch(tasks, expected)
+        del graph
+
+
 def test_batch_small_m_bit_exact() -> None:
     shapes = [(4, 4096, 64, 0, 64), (2, 2048, 40, 8, 32), (3, 256, 16, 0, 16), (1, 512, 33, 0, 33)]
     tasks, expected = _batch_case(32, shapes, fused_every=3)

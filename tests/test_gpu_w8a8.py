@@ -70,9 +70,9 @@ def test_fused_dequantize_fixture_bit_exact() -> None:
 @pytest.mark.parametrize(
     "m,n,k",
     [(1, 16, 16), (7, 33, 48), (129, 257, 64), (128, 128, 4096), (300, 1000, 1040), (1, 4096, 14336), (64, 14336, 4096),
-     # >= 256 tiles of 256 x 256 with K % 128 == 0: the large-tile streaming kernel,
-     # with partial edge tiles and one / two K stages.
-     (4000, 4100, 1024), (4096, 4096, 256), (4352, 4096, 128)],
+     # >= 256 tiles of 256 x 256 with K % 64 == 0: the large-tile kernel, with
+     # partial edge tiles (N % 4 != 0 among them) and one to three K stages.
+     (4000, 4100, 1024), (4096, 4096, 256), (4352, 4096, 128), (4096, 4098, 64), (4100, 4096, 192)],
 )
 def test_gemm_i32_random_shapes_exact(m: int, n: int, k: int) -> None:
     rng = np.random.default_rng(m * 7 + n * 3 + k)
@@ -94,6 +94,42 @@ def test_streaming_kernel_fused_epilogue_on_edge_tiles_bit_exact() -> None:
     rows = np.array([0, 1, 255, 256, 3839, 3840, 3999])
     expected = oracle.dequantize_epilogue(oracle.int8_gemm_i32(a[rows], w), sa[rows], sw, bias)
     np.testing.assert_array_equal(out[rows], expected)
+
+
+def test_large_tile_gemm_over_several_rounds_with_edge_tile_exact() -> None:
+    # 16 x 56 tiles of 256 x 256 (several rounds on a 256-CU device), the last
+    # column of tiles partial; int32 accumulators and the fused epilogue.
+    rng = np.random.default_rng(2720)
+    m, n, k = 4096, 14336 - 64, 128
+    a = rng.integers(-127, 128, size=(m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    out = gemm_int8.w8a8_gemm_i32(dev(a), dev(w)).cpu().numpy()
+    np.testing.assert_array_equal(out, oracle.int8_gemm_i32(a, w))
+    sa = rng.uniform(0.001, 0.1, m).astype(np.float32)
+    sw = rng.uniform(0.001, 0.1, n).astype(np.float32)
+    bias = rng.standard_normal(n, dtype=np.float32)
+    y = gemm_int8.w8a8_gemm_dequantize(dev(a), dev(w), dev(sa), dev(sw), dev(bias)).cpu().numpy()
+    np.testing.assert_array_equal(y, oracle.dequantize_epilogue(out, sa, sw, bias))
+
+
+def test_large_tile_epilogue_with_unaligned_output_rows_bit_exact() -> None:
+    # Output rows 4 * 4099 bytes apart: not 16-byte aligned, so the row-store
+    # epilogue writes element by element; the padding column stays untouched.
+    rng = np.random.default_rng(2719)
+    m, n, k = 4096, 4096, 128
+    a = rng.integers(-127, 128, size=(m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    sa = rng.uniform(0.001, 0.1, m).astype(np.float32)
+    sw = rng.uniform(0.001, 0.1, n).astype(np.float32)
+    bias = rng.standard_normal(n, dtype=np.float32)
+    storage = torch.full((m, n + 3), -7.0, dtype=torch.float32, device="cuda")
+    out = storage[:, :n]
+    gemm_int8.w8a8_gemm_dequantize(dev(a), dev(w), dev(sa), dev(sw), dev(bias), out=out)
+    got = storage.cpu().numpy()
+    rows = np.array([0, 3, 127, 128, 255, 2048, 4095])
+    expected = oracle.dequantize_epilogue(oracle.int8_gemm_i32(a[rows], w), sa[rows], sw, bias)
+    np.testing.assert_array_equal(got[rows, :n], expected)
+    np.testing.assert_array_equal(got[:, n:], -7.0)
 
 
 def test_gemm_i32_extreme_accumulators_exact() -> None:
