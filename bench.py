@@ -68,8 +68,8 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--legs", default="decode,w8a8,cfg0,cfg1,cfg2,copy,cpu")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of each CPU-baseline sample")
+    ap.add_argument("--legs", default="decode,w8a8,gemv,prefill,cfg0,cfg1,cfg2,copy,cpu")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of each CPU-baseline sample")
     return ap.parse_args()
 
 
@@ -119,6 +119,22 @@ class Runner:
             end.record(self.stream)
             torch.cuda.synchronize()
             wall = (time.perf_counter() - t0) * 1e3 / steps
+        return wall, start.elapsed_time(end) / steps
+
+    def timed_eager(self, steps: int, warmup: int) -> tuple[float, float]:
+        """(wall ms per step, event ms per step) of eager back-to-back launches."""
+        torch = self.torch
+        for _ in range(warmup):
+            self.run()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        start.record(self.stream)
+        for _ in range(steps):
+            self.run()
+        end.record(self.stream)
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3 / steps
         return wall, start.elapsed_time(end) / steps
 
     def kernel_times(self, repeats: int = 1) -> dict[str, list[float]]:
@@ -203,13 +219,20 @@ def leg_decode(torch, args) -> dict:
     torch.cuda.synchronize()
     times = runner.kernel_times(repeats=max(3, args.steps // 2))["q4_0_batch_kernel"]
     graph = runner.capture()
-    wall_ms, event_ms = runner.timed_graph(graph, args.steps, args.warmup)
+    graph_wall, graph_events = runner.timed_graph(graph, args.steps, args.warmup)
+    eager_wall, eager_events = runner.timed_eager(args.steps, args.warmup)
+    # The step is one launch either way; report the faster way of issuing it.
+    mode = "eager" if eager_wall <= graph_wall else "graph"
+    wall_ms, event_ms = (eager_wall, eager_events) if mode == "eager" else (graph_wall, graph_events)
     kernel_ms = float(np.mean(times))
     result["batched"] = {
         "launches_per_step": 1,
         "work_items": batch.work_items,
+        "launch_mode": mode,
         "ms_per_step_wall": wall_ms,
         "ms_per_step_events": event_ms,
+        "ms_per_step_wall_graph": graph_wall,
+        "ms_per_step_wall_eager": eager_wall,
         "gbs": bytes_step / (wall_ms * 1e-3) / 1e9,
         "kernel_avg_us": kernel_ms * 1e3,
         "kernel_min_us": float(np.min(times)) * 1e3,
@@ -391,6 +414,93 @@ def leg_w8a8(torch, args) -> dict:
     return result
 
 
+def leg_w8a8_gemv(torch, args) -> dict:
+    """Dynamic W8A8 at M = 1 (a decode token through the cfg4 FFN weights): the dot4 GEMV path.
+
+    HBM-bound on the int8 weights; the launches cycle through >= 512 MB of
+    distinct weight copies so every launch streams HBM.
+    """
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    out = {}
+    for label, (k, n) in {"gate_up": (4096, 14336), "down": (14336, 4096)}.items():
+        per = n * k
+        copies = max(2, -(-ROTATION_BYTES // per))
+        weights = []
+        from qpu_xla_amd.quantization import quantize_per_output_channel_int8
+
+        for _ in range(copies):
+            weights.append(quantize_per_output_channel_int8(torch.randn((n, k), generator=gen, device="cuda") * 0.02))
+        x = torch.randn((1, k), generator=gen, device="cuda")
+        bias = torch.randn((n,), generator=gen, device="cuda") * 0.1
+        qa = torch.empty((1, k), dtype=torch.int8, device="cuda")
+        sa = torch.empty((1,), dtype=torch.float32, device="cuda")
+        y = torch.empty((1, n), dtype=torch.float32, device="cuda")
+        runner = Runner(torch, torch.cuda.Stream())
+        for wt in weights:
+            runner.add("qxt_w8a8_linear", _p(x), _rs(x), _p(qa), _rs(qa), _p(sa), _p(wt.values), _rs(wt.values),
+                       _p(wt.scales), _p(bias), _p(y), _rs(y), 1, n, k, 0, 0, runner.handle)
+        runner.run()
+        torch.cuda.synchronize()
+        times = runner.kernel_times(repeats=2)
+        gemv_us = float(np.mean(times["w8a8_gemv_kernel"])) * 1e3
+        graph = runner.capture()
+        wall_ms, _ = runner.timed_graph(graph, max(2, args.steps // 4), 2)
+        b = n * k + k + 4 * n * 3  # int8 weights + int8 activation + sw, bias, y
+        out[label] = {
+            "shape": f"M=1 K={k} N={n}",
+            "copies": copies,
+            "gemv_kernel_us": gemv_us,
+            "gemv_kernel_gbs": b / (gemv_us * 1e-6) / 1e9,
+            "gemv_frac_hbm": b / (gemv_us * 1e-6) / 1e9 / PEAK_HBM_GBS,
+            "operator_us": wall_ms * 1e3 / copies,
+            "quantise_kernel_us": float(np.mean(times["rows_int8_kernel"])) * 1e3,
+        }
+        del graph, weights
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return out
+
+
+def leg_prefill(torch, args) -> dict:
+    """Q4_0 x Q8_0 prefill (M = 512 tokens) at the TinyLlama FFN shapes: the matrix-core path.
+
+    Every output needs, per 32-element block, an exact int32 dot (one MFMA per
+    32 x 32 outputs) and four fp32 VALU operations (convert, x dw, x da, add in
+    block order), so the kernel is bound by the non-packed fp32 VALU rate:
+    256 CU x 4 SIMD x 16 lanes x 2.4 GHz = 39.3 T operations/s.
+    """
+    from qpu_xla_amd.kernels.quantize import quantize_q4_0, quantize_q8_0
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(6)
+    rows = 512
+    valu_peak = 256 * 4 * 16 * 2.4e9
+    out = {}
+    for label, (k, n) in {"gate_up": (2048, 5632), "down": (5632, 2048)}.items():
+        wq = quantize_q4_0(torch.randn((n, k), generator=gen, device="cuda") * 0.02)
+        xq = quantize_q8_0(torch.randn((rows, k), generator=gen, device="cuda"))
+        y = torch.empty((rows, n), dtype=torch.float32, device="cuda")
+        runner = Runner(torch, torch.cuda.Stream())
+        runner.add("qxt_ggml_q4_0_q8_0_linear", _p(xq), _rs(xq), _p(wq), _rs(wq), _p(y), _rs(y),
+                   rows, k // 32, 0, 0, n, runner.handle)
+        runner.run()
+        torch.cuda.synchronize()
+        times = runner.kernel_times(repeats=5)["q4_0_tiled_kernel"]
+        us = float(np.mean(times)) * 1e3
+        valu_ops = rows * n * (k // 32) * 4
+        out[label] = {
+            "shape": f"M={rows} K={k} N={n}",
+            "kernel_us": us,
+            "tops": 2 * rows * n * k / (us * 1e-6) / 1e12,
+            "valu_bound_us": valu_ops / valu_peak * 1e6,
+            "frac_valu_bound": valu_ops / valu_peak / (us * 1e-6),
+        }
+        del wq, xq, y
+        torch.cuda.synchronize()
+    return out
+
+
 def leg_cfg1(torch, args) -> dict:
     """cfg1: W8A8 M=K=N=512 whole operator (launch-bound; parity case, reported only)."""
     gen = torch.Generator(device="cuda")
@@ -442,33 +552,38 @@ def leg_copy(torch) -> dict:
 
 
 def cpu_baseline_q4(budget_s: float) -> dict:
-    """The NumPy oracle (reference CPU path) on the cfg3 decode step, bounded by ``budget_s``."""
+    """The NumPy oracle (reference CPU path) on the cfg3 decode step, bounded by ``budget_s``.
+
+    Weights are prepared once (outside the timed region); the timed work is
+    Q8_0 quantisation + the Q4_0 x Q8_0 oracle of every linear, whole steps
+    repeated until the budget is spent.
+    """
     import oracle
 
     rng = np.random.default_rng(3)
-    done_bytes = 0
-    done = 0
-    elapsed = 0.0
-    linears = [(k, n) for _ in range(LAYERS) for (_, k, n) in TINYLLAMA_LAYER]
-    for k, n in linears:
-        w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
-        wq = oracle.quantize_q4_0_blocks(w)  # weight preparation: outside the timed region
-        x = rng.standard_normal((1, k), dtype=np.float32)
-        t0 = time.perf_counter()
-        xq = oracle.quantize_q8_0_blocks(x)
-        oracle.q4_0_q8_0_reference(xq, wq)
-        elapsed += time.perf_counter() - t0
-        done_bytes += q4_linear_bytes(1, k, n)
-        done += 1
+    linears = []
+    for _ in range(LAYERS):
+        for (_, k, n) in TINYLLAMA_LAYER:
+            w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+            linears.append((oracle.quantize_q4_0_blocks(w), rng.standard_normal((1, k), dtype=np.float32), k, n))
+    step_bytes = sum(q4_linear_bytes(1, k, n) for (_, _, k, n) in linears)
+    steps = 0
+    t0 = time.perf_counter()
+    while True:
+        for wq, x, _, _ in linears:
+            xq = oracle.quantize_q8_0_blocks(x)
+            oracle.q4_0_q8_0_reference(xq, wq)
+        steps += 1
+        elapsed = time.perf_counter() - t0
         if elapsed >= budget_s:
             break
     return {
-        "value": done_bytes / elapsed / 1e9,
+        "value": steps * step_bytes / elapsed / 1e9,
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"{done} of 154 cfg3 linears (Q8_0 quantise + Q4_0xQ8_0 oracle, NumPy single thread), "
-        f"{done_bytes / 1e6:.1f} MB in {elapsed:.2f} s",
+        "sample": f"{steps} whole cfg3 decode steps (154 linears: Q8_0 quantise + Q4_0xQ8_0 oracle, NumPy, "
+        f"single thread), {steps * step_bytes / 1e6:.1f} MB in {elapsed:.2f} s",
     }
 
 
@@ -484,7 +599,7 @@ def cpu_baseline_w8a8(budget_s: float) -> dict:
     bias = (rng.standard_normal(n, dtype=np.float32) * np.float32(0.1)).astype(np.float32)
     rows = 0
     elapsed = 0.0
-    while elapsed < budget_s and rows < 64:
+    while elapsed < budget_s and rows < 1024:
         x = rng.standard_normal((8, k), dtype=np.float32)
         t0 = time.perf_counter()
         qa, sa = oracle.quantize_rows_int8(x)
@@ -562,6 +677,14 @@ def main() -> int:
         log("leg w8a8 (cfg4)")
         out["w8a8"] = leg_w8a8(torch, args)
         log(f"w8a8: {out['w8a8']}")
+    if "gemv" in legs:
+        log("leg w8a8 gemv (M=1)")
+        out["gemv"] = leg_w8a8_gemv(torch, args)
+        log(f"gemv: {out['gemv']}")
+    if "prefill" in legs:
+        log("leg q4_0 prefill (M=512)")
+        out["prefill"] = leg_prefill(torch, args)
+        log(f"prefill: {out['prefill']}")
     if "cfg1" in legs:
         log("leg cfg1")
         out["cfg1"] = leg_cfg1(torch, args)
@@ -618,6 +741,8 @@ def main() -> int:
         ),
         "cpu_baseline": cpu,
         "w8a8": out.get("w8a8"),
+        "w8a8_gemv": out.get("gemv"),
+        "q4_0_prefill": out.get("prefill"),
         "w8a8_cpu_baseline": cpu_w8a8,
         "decode": decode,
         "configs": {key: out[key] for key in ("cfg0", "cfg1", "cfg2") if key in out},

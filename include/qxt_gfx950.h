@@ -143,7 +143,8 @@ int qxt_quantize_q4_0(const float *w, size_t w_row_stride, void *blocks, size_t 
  *   sum_b fl32(fl32(float(dot_b) * dw[wc, b]) * da[r, b]), summed in block order,
  * wc = weight_column_start + j, for r < rows, j < column_count.
  * activation: Q8_0 u8 [rows, blocks, 34]; weight: Q4_0 u8 [>= wc+1, blocks, 18].
- * Writes only destination[:, output_column_start : +column_count].
+ * Writes only destination[:, output_column_start : +column_count].  rows >= 16 run on the
+ * int8 matrix cores (one MFMA per 32 x 32 outputs and block), fewer rows on v_dot4.
  * Replaces GGML_Q4_0_Q8_0_LINEAR_KERNEL (src/qpu_xla/kernels/ggml_q4_0.py:783-841)
  * and the device work of qpu_llama_q4_0_linear_submit (qpu_llama_q4_0.h:72-75). */
 int qxt_ggml_q4_0_q8_0_linear(const void *activation, size_t activation_row_stride,
@@ -152,6 +153,28 @@ int qxt_ggml_q4_0_q8_0_linear(const void *activation, size_t activation_row_stri
                               uint32_t rows, uint32_t blocks,
                               uint32_t weight_column_start, uint32_t output_column_start,
                               uint32_t column_count, void *stream);
+
+/* Prefill Q4_0 x Q8_0 linear over the reference's split / tiled operand layout:
+ *   activation_q      int8 [rows, blocks*32] (the Q8_0 values, row stride in bytes, % 4 == 0),
+ *   activation_scales fp16 bits [rows, blocks], elements of activation_scale_bytes = 2 (uint16)
+ *                     or 4 (uint32 words holding the fp16 bits),
+ *   weight_q          uint32 [blocks*8, columns]: word (8b + g, n) = signed int8 values
+ *                     k = 4g .. 4g+3 of block b of column n (pack_ggml_q4_0_tiled_weights),
+ *   weight_scales     fp16 bits [blocks, columns] (uint16),
+ *   destination       fp32 [rows, columns].
+ * Result as qxt_ggml_q4_0_q8_0_linear (per-block exact int32 dots on the matrix cores, scaled
+ * by dw then da and summed in block order: bit-identical to ggml_q4_0_q8_0_reference).  Any
+ * rows / columns (the reference needs multiples of 16).  Replaces
+ * GGML_Q4_0_Q8_0_TILED_LINEAR_KERNEL (src/qpu_xla/kernels/ggml_q4_0.py:886-967) and its
+ * persistent variant (src/qpu_xla/kernels/ggml_q4_0_persistent.py:11), whose results are
+ * identical to the conventional launch. */
+int qxt_ggml_q4_0_q8_0_tiled_linear(const void *activation_q, size_t activation_q_row_stride,
+                                    const void *activation_scales, size_t activation_scales_row_stride,
+                                    uint32_t activation_scale_bytes, const void *weight_q,
+                                    size_t weight_q_row_stride, const void *weight_scales,
+                                    size_t weight_scales_row_stride, float *destination,
+                                    size_t destination_row_stride, uint32_t rows, uint32_t blocks,
+                                    uint32_t columns, void *stream);
 
 /* Debug twin of the linear above: dots[r, j, b] = exact int32 block dot of
  * row r with weight column weight_column_start + j (dots row stride

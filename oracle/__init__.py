@@ -23,6 +23,8 @@ Pinning status (what each function is checked against, in ``tests/``):
   RNE scale) and exact half-way ties that separate ``rint`` from ``round``.
 * W8A8: closed-form KAT (qpu_llama_w8a8_smoke.c:58-66), int64 brute force,
   quantiser invariants including the 1/127 scale floor.
+* ``pack_q4_0_tiled_weights`` / ``split_q8_0_blocks``: byte-level checks of
+  the word layout against the native blocks and exact inversion.
 * ``quantize_q4_0_blocks``: PARITY UNPINNED against upstream ggml
   ``quantize_row_q4_0`` (ggml is not vendored in the reference); only the
   BASELINE formula's invariants are checked.
@@ -33,12 +35,14 @@ from oracle.ggml import (  # noqa: F401
     Q8_0_BLOCK_BYTES,
     QK,
     pack_q4_0_blocks,
+    pack_q4_0_tiled_weights,
     pack_q8_0_blocks,
     q4_0_q8_0_block_dots,
     q4_0_q8_0_reference,
     quantize_q4_0_blocks,
     quantize_q8_0_blocks,
     quantize_q8_0_split,
+    split_q8_0_blocks,
     unpack_q4_0_blocks,
     unpack_q8_0_blocks,
 )

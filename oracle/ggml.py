@@ -195,3 +195,32 @@ def quantize_q4_0_blocks(weights: np.ndarray) -> np.ndarray:
     shifted = (grouped * inverse[..., None]) + np.float32(8.5)
     codes = np.minimum(np.trunc(shifted), 15).astype(np.uint8)
     return pack_q4_0_blocks(d.astype(np.float16), codes)
+
+
+def pack_q4_0_tiled_weights(blocks: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Native Q4_0 weights [N, B, 18] -> (fp16 scale bits uint16 [B, N], uint32 words [B * 8, N]).
+
+    Follows ``src/qpu_xla/kernels/ggml_q4_0.py:844-855``: word ``(8 b + g, n)``
+    holds the signed values ``code - 8`` of elements ``4 g .. 4 g + 3`` of
+    block ``b`` of output ``n`` as little-endian int8 bytes.
+    """
+    scales, values = unpack_q4_0_blocks(blocks)
+    if blocks.ndim != 3:
+        raise ValueError("native Q4_0 weights must have shape (outputs, blocks, 18)")
+    scale_words = np.ascontiguousarray(scales.astype(np.float16).T.view(np.uint16))
+    outputs, reduction_blocks, _ = values.shape
+    groups = np.ascontiguousarray(values.astype(np.int8).reshape(outputs, reduction_blocks, 8, 4).transpose(1, 2, 0, 3))
+    return scale_words, np.ascontiguousarray(groups.view(np.uint32).reshape(reduction_blocks * 8, outputs))
+
+
+def split_q8_0_blocks(blocks: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Native Q8_0 activations [M, B, 34] -> (fp16 scale bits uint16 [M, B], int8 values as uint8 [M, B * 32]).
+
+    The split activation operands of the reference's tiled tests
+    (``tests/test_qpu_xla_ggml_q4_0.py:97-98``).
+    """
+    rows, nblocks, _ = blocks.shape
+    scales = np.ascontiguousarray(blocks[..., :2]).view(np.uint16).reshape(rows, nblocks)
+    values = np.ascontiguousarray(blocks[..., 2:].reshape(rows, nblocks * QK))
+    return scales, values
+

@@ -54,6 +54,15 @@ int launch(const char *name, void (*kernel)(KArgs...), dim3 grid, dim3 block, si
     return launch_status(name);
 }
 
+// Native-layout Q4_0 x Q8_0 linear for rows >= 16 on the int8 matrix cores
+// (qxt_q4_0_tiled.hip); same contract and result as the small-M kernel.
+bool q4_0_tiled_native_supported(size_t act_stride, size_t w_stride, uint32_t rows, uint32_t blocks,
+                                 uint32_t weight_column_start, uint32_t column_count);
+int q4_0_tiled_native(const void *activation, size_t activation_row_stride, const void *weight,
+                      size_t weight_row_stride, float *destination, size_t destination_row_stride, uint32_t rows,
+                      uint32_t blocks, uint32_t weight_column_start, uint32_t output_column_start,
+                      uint32_t column_count, hipStream_t stream);
+
 // -------------------------------------------------------------- device side
 
 constexpr int QK = 32;            // elements per GGML block

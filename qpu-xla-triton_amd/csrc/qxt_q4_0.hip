@@ -486,6 +486,12 @@ int qxt_ggml_q4_0_q8_0_linear(const void *activation, size_t activation_row_stri
         return fail(QXT_INVALID_ARGUMENT, "q4_0 linear: column range overflows");
     rc = injected(QXT_FAIL_SUBMISSION);
     if (rc != QXT_OK) return rc;
+    // Prefill-sized row counts run on the int8 matrix cores (bit-identical result).
+    if (q4_0_tiled_native_supported(activation_row_stride, weight_row_stride, rows, blocks, weight_column_start,
+                                    column_count))
+        return q4_0_tiled_native(activation, activation_row_stride, weight, weight_row_stride, destination,
+                                 destination_row_stride, rows, blocks, weight_column_start, output_column_start,
+                                 column_count, as_stream(stream));
     Q4Task t{};
     t.act = static_cast<const uint8_t *>(activation);
     t.act_stride = activation_row_stride;

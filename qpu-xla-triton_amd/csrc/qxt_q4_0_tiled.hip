@@ -1,0 +1,348 @@
+// Q4_0 x Q8_0 prefill linear (M >= 16) on the int8 matrix cores of gfx950.
+//
+// Arithmetic is that of the reference oracle ggml_q4_0_q8_0_reference
+// (src/qpu_xla/kernels/ggml_q4_0.py:81-100): per 32-element block an exact
+// int32 dot, then c_b = fl32(fl32(float(dot_b) * dw_b) * da_b), summed in
+// block order.  One v_mfma_i32_32x32x32_i8 computes the exact block dots of
+// a 32 x 32 output tile for one block (K = 32 = one GGML block), and the
+// lane that receives each dot applies that block's two scales and adds the
+// term to its fp32 accumulator before the next block's dots arrive, so the
+// result is bit-identical to the oracle.  (The reference's own tiled QPU
+// program, ggml_q4_0.py:309-547, multiplies by the activation scale first
+// and is checked against the oracle within rtol 2e-6; this kernel matches
+// the oracle exactly.)
+//
+// The four VALU operations per output and block (convert, two multiplies,
+// add) bound the kernel, not the matrix core: one 32 x 32 x 32 MFMA per
+// wave per block feeds 64 VALU instructions.  A 256-thread workgroup owns a
+// 64 x 64 output tile (four waves of 32 x 32); block scales are staged in
+// LDS as fp32 32 blocks at a time; the operand fragments of the next four
+// blocks are in flight while one block is reduced.
+//
+// Two operand layouts:
+//   * split (the reference's GGML_Q4_0_Q8_0_TILED_LINEAR_KERNEL contract,
+//     ggml_q4_0.py:844-967): activation int8 [M, K] + fp16 scales [M, B]
+//     (2-byte halves or 4-byte words), weight uint32 [B * 8, N] of signed
+//     int8 quads (pack_ggml_q4_0_tiled_weights) + fp16 scales [B, N];
+//   * native 34-byte Q8_0 / 18-byte Q4_0 blocks (the linear's own layout).
+#include "qxt_common.h"
+
+namespace qxt {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kTile = 64;   // output rows and columns per workgroup
+constexpr int kChunk = 32;  // blocks of scales staged per LDS round
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kOutOfRange = 0x80000000u;  // operands are < 2 GiB: always out of range
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, 0x00020000);
+}
+
+struct TiledArgs {
+    // split layout
+    const uint8_t *aq;   // int8 [M, K]
+    const uint8_t *as;   // fp16 scales [M, B] as 2- or 4-byte elements
+    const uint8_t *wq;   // uint32 [B * 8, N]
+    const uint8_t *ws;   // fp16 scales [B, N]
+    // native layout
+    const uint8_t *act;  // Q8_0 [M, B, 34]
+    const uint8_t *w;    // Q4_0 [>= wcol0 + N, B, 18]
+    float *y;
+    uint32_t aq_stride, as_stride, as_bytes, wq_stride, ws_stride, act_stride, w_stride;
+    size_t y_stride;
+    uint32_t a_extent, w_extent, as_extent, ws_extent;  // buffer-descriptor ranges
+    int m, n, blocks, wcol0, ocol0;
+};
+
+// fp16 bits at a 2-byte aligned offset (0 out of range).
+__device__ __forceinline__ float load_half(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return half_bits_to_float(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+}
+
+// Nibble codes 0..15 of one k half (low nibbles for h = 0, high for h = 1)
+// as signed int8 code - 8, four per word: (v | 0x80) - 8 never borrows
+// across bytes, and ^ 0x80 turns 0x78..0x87 into -8..7.
+__device__ __forceinline__ v4i nibbles_to_int8(v4u x, int h) {
+    v4i out;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t v = (h ? (x[i] >> 4) : x[i]) & 0x0F0F0F0Fu;
+        out[i] = static_cast<int>(((v | 0x80808080u) - 0x08080808u) ^ 0x80808080u);
+    }
+    return out;
+}
+
+// Raw loads of one block's fragments for this lane, consumed later by
+// frags_of(): A = 16 activation bytes of row `am` (k half h), W = the 16
+// weight bytes of column `bn` needed for k half h.  Native blocks sit at
+// 2-byte aligned offsets: the loads cover the aligned dwords around them
+// (dwordx4 at off & ~3, then 2 bytes at (off & ~3) + 16) and alignbyte by
+// off & 3 (0 or 2) picks the 16 bytes, so no load result is needed at issue
+// time and no load reaches past byte off + 15 of a fragment that ends a
+// tensor when off is not 4-byte aligned (an aligned fragment's extra 2-byte
+// load falls outside the descriptor range and returns zero, unused).
+struct RawFrags {
+    v4u a, w;
+    uint32_t a_hi, w_hi, a_shift, w_shift;
+};
+
+template <bool NATIVE>
+__device__ __forceinline__ void issue_frags(const TiledArgs &t, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rw,
+                                            int am, int bn, bool a_ok, bool b_ok, int h, int b, RawFrags &f) {
+    // Past the last block (and for rows / columns outside the matrix) the
+    // offsets fall outside the descriptor range: zeros, no memory traffic,
+    // and no branch, so every refill issues the same loads.
+    const bool in_k = b < t.blocks;
+    if constexpr (NATIVE) {
+        const uint32_t ao =
+            a_ok && in_k ? static_cast<uint32_t>(am) * t.act_stride + b * 34 + 2 + 16 * h : kOutOfRange;
+        const uint32_t wo =
+            b_ok && in_k ? static_cast<uint32_t>(t.wcol0 + bn) * t.w_stride + b * 18 + 2 : kOutOfRange;
+        f.a = __builtin_amdgcn_raw_buffer_load_b128(ra, ao & ~3u, 0, 0);
+        f.a_hi = __builtin_amdgcn_raw_buffer_load_b16(ra, (ao & ~3u) + 16, 0, 0);
+        f.w = __builtin_amdgcn_raw_buffer_load_b128(rw, wo & ~3u, 0, 0);
+        f.w_hi = __builtin_amdgcn_raw_buffer_load_b16(rw, (wo & ~3u) + 16, 0, 0);
+        f.a_shift = ao & 3u;
+        f.w_shift = wo & 3u;
+    } else {
+        f.a = __builtin_amdgcn_raw_buffer_load_b128(
+            ra, a_ok && in_k ? static_cast<uint32_t>(am) * t.aq_stride + b * 32 + 16 * h : kOutOfRange, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            f.w[i] = __builtin_amdgcn_raw_buffer_load_b32(
+                rw, b_ok && in_k ? static_cast<uint32_t>(b * 8 + 4 * h + i) * t.wq_stride + bn * 4 : kOutOfRange, 0,
+                0);
+    }
+}
+
+__device__ __forceinline__ v4u realign(v4u lo, uint32_t hi, uint32_t shift) {
+    v4u out;
+    out[0] = __builtin_amdgcn_alignbyte(lo[1], lo[0], shift);
+    out[1] = __builtin_amdgcn_alignbyte(lo[2], lo[1], shift);
+    out[2] = __builtin_amdgcn_alignbyte(lo[3], lo[2], shift);
+    out[3] = __builtin_amdgcn_alignbyte(hi, lo[3], shift);
+    return out;
+}
+
+template <bool NATIVE>
+__device__ __forceinline__ void frags_of(const RawFrags &f, int h, v4i &a, v4i &w) {
+    if constexpr (NATIVE) {
+        const v4u ar = realign(f.a, f.a_hi, f.a_shift);
+        a = v4i{static_cast<int>(ar[0]), static_cast<int>(ar[1]), static_cast<int>(ar[2]), static_cast<int>(ar[3])};
+        w = nibbles_to_int8(realign(f.w, f.w_hi, f.w_shift), h);
+    } else {
+        a = v4i{static_cast<int>(f.a[0]), static_cast<int>(f.a[1]), static_cast<int>(f.a[2]), static_cast<int>(f.a[3])};
+        w = v4i{static_cast<int>(f.w[0]), static_cast<int>(f.w[1]), static_cast<int>(f.w[2]), static_cast<int>(f.w[3])};
+    }
+}
+
+constexpr int kAhead = 4;  // blocks of fragments in flight ahead of the one being reduced
+
+template <bool NATIVE>
+__global__ __launch_bounds__(kThreads) void q4_0_tiled_kernel(TiledArgs t) {
+    __shared__ __attribute__((aligned(16))) float s_da[kChunk][kTile];
+    __shared__ __attribute__((aligned(16))) float s_dw[kChunk][kTile];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * kTile, n0 = blockIdx.x * kTile;
+    const int h = lane >> 5, l32 = lane & 31;
+    const int am = m0 + wm * 32 + l32;  // row of this lane's A fragment
+    const int bn = n0 + wn * 32 + l32;  // column of this lane's B fragment (and of its outputs)
+    const bool a_ok = am < t.m, b_ok = bn < t.n;
+
+    const __amdgpu_buffer_rsrc_t ra = rsrc(NATIVE ? t.act : t.aq, t.a_extent);
+    const __amdgpu_buffer_rsrc_t rw = rsrc(NATIVE ? t.w : t.wq, t.w_extent);
+    const __amdgpu_buffer_rsrc_t ras = rsrc(NATIVE ? t.act : t.as, NATIVE ? t.a_extent : t.as_extent);
+    const __amdgpu_buffer_rsrc_t rws = rsrc(NATIVE ? t.w : t.ws, NATIVE ? t.w_extent : t.ws_extent);
+
+    float acc[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+
+    // Ring of fragment registers: slot j holds block b with b % kAhead == j.
+    RawFrags ring[kAhead];
+#pragma unroll
+    for (int j = 0; j < kAhead; ++j) issue_frags<NATIVE>(t, ra, rw, am, bn, a_ok, b_ok, h, j, ring[j]);
+
+    for (int c0 = 0; c0 < t.blocks; c0 += kChunk) {
+        __syncthreads();  // the previous chunk's scales are consumed
+        // Scales of blocks c0 .. c0 + kChunk - 1 for the tile's rows and
+        // columns (zeros past M, N or K through out-of-range offsets), all
+        // loads issued before any is used.
+        constexpr int kPer = kChunk * kTile / kThreads;
+        uint32_t da_bits[kPer], dw_bits[kPer];
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+            const int i = threadIdx.x + u * kThreads;
+            const int cb = i / kTile, r = i - cb * kTile, b = c0 + cb;
+            const int m = m0 + r, n = n0 + r;
+            const bool in_k = b < t.blocks;
+            uint32_t ao, wo;
+            if constexpr (NATIVE) {
+                ao = in_k && m < t.m ? static_cast<uint32_t>(m) * t.act_stride + b * 34 : kOutOfRange;
+                wo = in_k && n < t.n ? static_cast<uint32_t>(t.wcol0 + n) * t.w_stride + b * 18 : kOutOfRange;
+            } else {
+                ao = in_k && m < t.m ? static_cast<uint32_t>(m) * t.as_stride + b * t.as_bytes : kOutOfRange;
+                wo = in_k && n < t.n ? static_cast<uint32_t>(b) * t.ws_stride + n * 2 : kOutOfRange;
+            }
+            da_bits[u] = __builtin_amdgcn_raw_buffer_load_b16(ras, ao, 0, 0);
+            dw_bits[u] = __builtin_amdgcn_raw_buffer_load_b16(rws, wo, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+            const int i = threadIdx.x + u * kThreads;
+            const int cb = i / kTile, r = i - cb * kTile;
+            s_da[cb][r] = half_bits_to_float(da_bits[u]);
+            s_dw[cb][r] = half_bits_to_float(dw_bits[u]);
+        }
+        __syncthreads();
+        // Groups of kAhead blocks, the tail padded with blocks past K whose
+        // fragments and scales are zero: their terms are exactly +0, and the
+        // accumulator, which starts at +0, never holds -0, so adding them
+        // changes nothing.
+        const int nb = min(kChunk, t.blocks - c0);
+        for (int cb0 = 0; cb0 < nb; cb0 += kAhead) {
+#pragma unroll
+            for (int j = 0; j < kAhead; ++j) {
+                const int cb = cb0 + j;
+                {
+                    v4i af, wf;
+                    frags_of<NATIVE>(ring[j], h, af, wf);
+                    const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, wf, zero, 0, 0, 0);
+                    // Refill the slot with the block kAhead further on.
+                    issue_frags<NATIVE>(t, ra, rw, am, bn, a_ok, b_ok, h, c0 + cb + kAhead, ring[j]);
+                    const float dw = s_dw[cb][wn * 32 + l32];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float4 da4 = *reinterpret_cast<const float4 *>(&s_da[cb][wm * 32 + 8 * q + 4 * h]);
+                        const float das[4] = {da4.x, da4.y, da4.z, da4.w};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            float v = static_cast<float>(d[4 * q + e]) * dw;
+                            v = v * das[e];
+                            acc[4 * q + e] = acc[4 * q + e] + v;
+                        }
+                    }
+                }
+            }
+        }
+    }
+    if (!b_ok) return;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int m = m0 + wm * 32 + 8 * q + 4 * h + e;
+            if (m < t.m)
+                reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(t.y) + static_cast<size_t>(m) * t.y_stride)[t.ocol0 + bn] =
+                    acc[4 * q + e];
+        }
+}
+
+int launch_tiled(const TiledArgs &t, bool native, hipStream_t stream) {
+    const dim3 grid((t.n + kTile - 1) / kTile, (t.m + kTile - 1) / kTile, 1);
+    if (grid.y > 65535u) return fail(QXT_INVALID_ARGUMENT, "q4_0 tiled linear: too many rows");
+    if (native) return launch("q4_0_tiled_kernel", q4_0_tiled_kernel<true>, grid, dim3(kThreads), 0, stream, t);
+    return launch("q4_0_tiled_kernel", q4_0_tiled_kernel<false>, grid, dim3(kThreads), 0, stream, t);
+}
+
+bool below_2gib(uint64_t bytes) { return bytes < (1ull << 31); }
+
+}  // namespace
+
+bool q4_0_tiled_native_supported(size_t act_stride, size_t w_stride, uint32_t rows, uint32_t blocks,
+                                 uint32_t weight_column_start, uint32_t column_count) {
+    const uint64_t a_extent = static_cast<uint64_t>(rows - 1) * act_stride + static_cast<uint64_t>(blocks) * 34;
+    const uint64_t w_extent =
+        static_cast<uint64_t>(weight_column_start + column_count - 1) * w_stride + static_cast<uint64_t>(blocks) * 18;
+    return rows >= 16 && below_2gib(a_extent) && below_2gib(w_extent);
+}
+
+int q4_0_tiled_native(const void *activation, size_t activation_row_stride, const void *weight,
+                      size_t weight_row_stride, float *destination, size_t destination_row_stride, uint32_t rows,
+                      uint32_t blocks, uint32_t weight_column_start, uint32_t output_column_start,
+                      uint32_t column_count, hipStream_t stream) {
+    TiledArgs t{};
+    t.act = static_cast<const uint8_t *>(activation);
+    t.w = static_cast<const uint8_t *>(weight);
+    t.y = destination;
+    t.act_stride = static_cast<uint32_t>(activation_row_stride);
+    t.w_stride = static_cast<uint32_t>(weight_row_stride);
+    t.y_stride = destination_row_stride;
+    t.a_extent = static_cast<uint32_t>(static_cast<uint64_t>(rows - 1) * activation_row_stride + blocks * 34ull);
+    t.w_extent = static_cast<uint32_t>(static_cast<uint64_t>(weight_column_start + column_count - 1) * weight_row_stride +
+                                       blocks * 18ull);
+    t.m = static_cast<int>(rows);
+    t.n = static_cast<int>(column_count);
+    t.blocks = static_cast<int>(blocks);
+    t.wcol0 = static_cast<int>(weight_column_start);
+    t.ocol0 = static_cast<int>(output_column_start);
+    return launch_tiled(t, true, stream);
+}
+
+}  // namespace qxt
+
+using namespace qxt;
+
+extern "C" int qxt_ggml_q4_0_q8_0_tiled_linear(const void *activation_q, size_t activation_q_row_stride,
+                                               const void *activation_scales, size_t activation_scales_row_stride,
+                                               uint32_t activation_scale_bytes, const void *weight_q,
+                                               size_t weight_q_row_stride, const void *weight_scales,
+                                               size_t weight_scales_row_stride, float *destination,
+                                               size_t destination_row_stride, uint32_t rows, uint32_t blocks,
+                                               uint32_t columns, void *stream) {
+    if (activation_q == nullptr || activation_scales == nullptr || weight_q == nullptr || weight_scales == nullptr ||
+        destination == nullptr)
+        return fail(QXT_INVALID_ARGUMENT, "q4_0 tiled linear: null pointer");
+    if (rows == 0 || blocks == 0 || columns == 0)
+        return fail(QXT_INVALID_ARGUMENT, "q4_0 tiled linear: rows, blocks and columns must be positive");
+    if (activation_scale_bytes != 2 && activation_scale_bytes != 4)
+        return fail(QXT_INVALID_ARGUMENT, "q4_0 tiled linear: activation scales are 2- or 4-byte elements");
+    const uint64_t k = static_cast<uint64_t>(blocks) * 32;
+    if (activation_q_row_stride < k || activation_q_row_stride % 4 || !aligned(activation_q, 4) ||
+        activation_scales_row_stride < static_cast<uint64_t>(blocks) * activation_scale_bytes ||
+        activation_scales_row_stride % activation_scale_bytes || !aligned(activation_scales, activation_scale_bytes) ||
+        weight_q_row_stride < static_cast<uint64_t>(columns) * 4 || weight_q_row_stride % 4 || !aligned(weight_q, 4) ||
+        weight_scales_row_stride < static_cast<uint64_t>(columns) * 2 || weight_scales_row_stride % 2 ||
+        !aligned(weight_scales, 2))
+        return fail(QXT_INVALID_ARGUMENT, "q4_0 tiled linear: bad operand strides or alignment");
+    if (!aligned(destination, 4) || destination_row_stride % 4 ||
+        destination_row_stride < static_cast<uint64_t>(columns) * 4)
+        return fail(QXT_INVALID_ARGUMENT, "q4_0 tiled linear: bad destination");
+    const uint64_t a_extent = static_cast<uint64_t>(rows - 1) * activation_q_row_stride + k;
+    const uint64_t as_extent =
+        static_cast<uint64_t>(rows - 1) * activation_scales_row_stride + static_cast<uint64_t>(blocks) * activation_scale_bytes;
+    const uint64_t w_extent = static_cast<uint64_t>(blocks * 8ull - 1) * weight_q_row_stride + columns * 4ull;
+    const uint64_t ws_extent = static_cast<uint64_t>(blocks - 1) * weight_scales_row_stride + columns * 2ull;
+    if (!below_2gib(a_extent) || !below_2gib(as_extent) || !below_2gib(w_extent) || !below_2gib(ws_extent))
+        return fail(QXT_INVALID_ARGUMENT, "q4_0 tiled linear: operands must be smaller than 2 GiB");
+    int rc = injected(QXT_FAIL_SUBMISSION);
+    if (rc != QXT_OK) return rc;
+    TiledArgs t{};
+    t.aq = static_cast<const uint8_t *>(activation_q);
+    t.as = static_cast<const uint8_t *>(activation_scales);
+    t.wq = static_cast<const uint8_t *>(weight_q);
+    t.ws = static_cast<const uint8_t *>(weight_scales);
+    t.y = destination;
+    t.aq_stride = static_cast<uint32_t>(activation_q_row_stride);
+    t.as_stride = static_cast<uint32_t>(activation_scales_row_stride);
+    t.as_bytes = activation_scale_bytes;
+    t.wq_stride = static_cast<uint32_t>(weight_q_row_stride);
+    t.ws_stride = static_cast<uint32_t>(weight_scales_row_stride);
+    t.y_stride = destination_row_stride;
+    t.a_extent = static_cast<uint32_t>(a_extent);
+    t.as_extent = static_cast<uint32_t>(as_extent);
+    t.w_extent = static_cast<uint32_t>(w_extent);
+    t.ws_extent = static_cast<uint32_t>(ws_extent);
+    t.m = static_cast<int>(rows);
+    t.n = static_cast<int>(columns);
+    t.blocks = static_cast<int>(blocks);
+    return launch_tiled(t, false, as_stream(stream));
+}

@@ -582,6 +582,137 @@ __global__ __launch_bounds__(kThreads) void w8a8_gemm_stream_kernel(GemmArgs arg
     epilogue_256<EPI>(args, acc, m0, n0, wm, wn, lane, smem);
 }
 
+// ----------------------------------------------------------------------------
+// GEMV path (M <= 4): HBM-bound streaming of the weight with v_dot4_i32_i8,
+// no MFMA.  The activation rows (M x K int8) are staged in LDS once per
+// workgroup.  Integer sums are exact in any order, so the results equal the
+// MFMA kernels' bit for bit.
+
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) v += __shfl_xor(v, s, 64);
+    return v;
+}
+
+template <int EPI>
+__device__ __forceinline__ void store_one(const GemmArgs &args, int row, int col, int acc) {
+    if constexpr (EPI == EPI_I32) {
+        reinterpret_cast<int32_t *>(reinterpret_cast<uint8_t *>(args.acc) + static_cast<size_t>(row) * args.ldacc)[col] =
+            acc;
+    } else {
+        float y = static_cast<float>(acc) * args.sa[row];
+        y = y * args.sw[col];
+        if constexpr (EPI == EPI_DEQUANT_BIAS) y = y + args.bias[col];
+        reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(args.y) + static_cast<size_t>(row) * args.ldy)[col] = y;
+    }
+}
+
+// Stage activation rows [0, MR) (zeros past M) as 16-byte chunks in LDS.
+template <int MR>
+__device__ __forceinline__ void stage_rows(const GemmArgs &args, v4u *act) {
+    const int k16 = args.k / 16;
+    const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(args.a, args.a_bytes);
+    for (int i = threadIdx.x; i < MR * k16; i += kThreads) {
+        const int r = i / k16, c = i - r * k16;
+        const uint32_t off = r < args.m ? static_cast<uint32_t>(r) * args.lda + c * 16 : kOutOfRange;
+        act[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
+    }
+    __syncthreads();
+}
+
+// Weight [N, K] (K contiguous): each wave owns 4 output columns and streams
+// their K bytes 1 KB per load instruction (lane l takes bytes 16 l .. 16 l + 15
+// of each kilobyte), then reduces across the wave.
+constexpr int kGemvColsNK = 16;  // per workgroup: 4 waves x 4 columns
+template <int MR, int EPI>
+__global__ __launch_bounds__(kThreads) void w8a8_gemv_nk_kernel(GemmArgs args) {
+    extern __shared__ v4u act[];  // [MR][K / 16]
+    stage_rows<MR>(args, act);
+    const int k16 = args.k / 16;
+    const int lane = threadIdx.x & 63;
+    const int n0 = blockIdx.x * kGemvColsNK + (threadIdx.x >> 6) * 4;
+    const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(args.w, args.w_bytes);
+    uint32_t row_off[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) row_off[j] = n0 + j < args.n ? static_cast<uint32_t>(n0 + j) * args.ldw : kOutOfRange;
+    int acc[4][MR];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < MR; ++r) acc[j][r] = 0;
+#pragma unroll 2
+    for (int c = lane; c < k16; c += 64) {
+        v4u wv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            wv[j] = __builtin_amdgcn_raw_buffer_load_b128(rb, row_off[j] == kOutOfRange ? kOutOfRange : row_off[j] + c * 16,
+                                                          0, 0);
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+            const v4u av = act[r * k16 + c];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                int s = acc[j][r];
+                s = dot4(static_cast<int>(wv[j][0]), static_cast<int>(av[0]), s);
+                s = dot4(static_cast<int>(wv[j][1]), static_cast<int>(av[1]), s);
+                s = dot4(static_cast<int>(wv[j][2]), static_cast<int>(av[2]), s);
+                s = dot4(static_cast<int>(wv[j][3]), static_cast<int>(av[3]), s);
+                acc[j][r] = s;
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < MR; ++r) acc[j][r] = wave_sum(acc[j][r]);
+    if (lane == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < MR; ++r)
+                if (n0 + j < args.n && r < args.m) store_one<EPI>(args, r, n0 + j, acc[j][r]);
+    }
+}
+
+// Weight packed K4 [K/4, N] uint32 (pack_int8_quads(W).T): lane l of every
+// wave owns column n0 + l; the four waves split K and add their exact
+// partial sums through LDS.
+constexpr int kGemvColsK4N = 64;
+template <int MR, int EPI>
+__global__ __launch_bounds__(kThreads) void w8a8_gemv_k4n_kernel(GemmArgs args) {
+    extern __shared__ v4u act[];  // [MR][K / 16]
+    __shared__ int part[4][MR][64];
+    stage_rows<MR>(args, act);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = blockIdx.x * kGemvColsK4N + lane;
+    const int k4 = args.k / 4;
+    const int per = (k4 + 3) / 4;
+    const int q0 = wave * per, q1 = min(k4, q0 + per);
+    const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(args.w, args.w_bytes);
+    const uint32_t col_off = col < args.n ? static_cast<uint32_t>(col) * 4 : kOutOfRange;
+    const uint32_t *aw = reinterpret_cast<const uint32_t *>(act);
+    int acc[MR];
+#pragma unroll
+    for (int r = 0; r < MR; ++r) acc[r] = 0;
+#pragma unroll 8
+    for (int q = q0; q < q1; ++q) {
+        const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(
+            rb, col_off == kOutOfRange ? kOutOfRange : static_cast<uint32_t>(q) * args.ldw + col_off, 0, 0);
+#pragma unroll
+        for (int r = 0; r < MR; ++r) acc[r] = dot4(static_cast<int>(w), static_cast<int>(aw[r * k4 + q]), acc[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < MR; ++r) part[wave][r][lane] = acc[r];
+    __syncthreads();
+    if (wave == 0 && col < args.n) {
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+            const int s = part[0][r][lane] + part[1][r][lane] + part[2][r][lane] + part[3][r][lane];
+            if (r < args.m) store_one<EPI>(args, r, col, s);
+        }
+    }
+}
+
 __global__ __launch_bounds__(kThreads) void dequantize_kernel(const int32_t *__restrict__ acc, size_t ldacc,
                                                               const float *__restrict__ sa,
                                                               const float *__restrict__ sw,
@@ -632,7 +763,40 @@ int launch_stream(const GemmArgs &args, int epi, hipStream_t stream) {
     return launch("w8a8_gemm_kernel", kernel, grid, dim3(kThreads), 0, stream, a2);
 }
 
+template <int MR>
+int launch_gemv(GemmArgs args, int epi, uint32_t layout, hipStream_t stream) {
+    args.a_bytes = static_cast<uint32_t>(static_cast<size_t>(args.m - 1) * args.lda + args.k);
+    const size_t lds = static_cast<size_t>(MR) * args.k;
+    if (layout == QXT_W8A8_WEIGHT_K4N) {
+        args.w_bytes = static_cast<uint32_t>(static_cast<size_t>(args.k / 4 - 1) * args.ldw + args.n * 4);
+        auto kernel = epi == EPI_I32        ? w8a8_gemv_k4n_kernel<MR, EPI_I32>
+                      : epi == EPI_DEQUANT ? w8a8_gemv_k4n_kernel<MR, EPI_DEQUANT>
+                                           : w8a8_gemv_k4n_kernel<MR, EPI_DEQUANT_BIAS>;
+        return launch("w8a8_gemv_kernel", kernel, dim3((args.n + kGemvColsK4N - 1) / kGemvColsK4N), dim3(kThreads), lds,
+                      stream, args);
+    }
+    args.w_bytes = static_cast<uint32_t>(static_cast<size_t>(args.n - 1) * args.ldw + args.k);
+    auto kernel = epi == EPI_I32        ? w8a8_gemv_nk_kernel<MR, EPI_I32>
+                  : epi == EPI_DEQUANT ? w8a8_gemv_nk_kernel<MR, EPI_DEQUANT>
+                                       : w8a8_gemv_nk_kernel<MR, EPI_DEQUANT_BIAS>;
+    return launch("w8a8_gemv_kernel", kernel, dim3((args.n + kGemvColsNK - 1) / kGemvColsNK), dim3(kThreads), lds,
+                  stream, args);
+}
+
+// Rows up to which the GEMV path runs; its activation rows (padded to 1, 2
+// or 4) must fit the 60 KB of dynamic LDS it stages them in.
+constexpr int kGemvMaxRows = 4;
+constexpr size_t kGemvMaxLds = 60 * 1024;
+
 int run_gemm(const GemmArgs &args, int epi, uint32_t layout, hipStream_t stream) {
+    const int gemv_rows = args.m <= 2 ? args.m : 4;
+    if (args.m <= kGemvMaxRows && static_cast<size_t>(gemv_rows) * args.k <= kGemvMaxLds) {
+        switch (args.m) {
+            case 1: return launch_gemv<1>(args, epi, layout, stream);
+            case 2: return launch_gemv<2>(args, epi, layout, stream);
+            default: return launch_gemv<4>(args, epi, layout, stream);
+        }
+    }
     // 256 x 256 tiles once they give every CU a workgroup; 128 x 128 below that.
     const long cus = compute_units();
     const long tm = (args.m + 255) / 256, tn = (args.n + 255) / 256;

@@ -95,6 +95,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "qxt_quantize_q4_0": (c_int, [_P, _SZ, _P, _SZ, _U, _U, _P]),
     "qxt_ggml_q4_0_q8_0_linear": (c_int, [_P, _SZ, _P, _SZ, _P, _SZ, _U, _U, _U, _U, _U, _P]),
     "qxt_ggml_q4_0_q8_0_block_dots": (c_int, [_P, _SZ, _P, _SZ, _P, _U, _U, _U, _U, _P]),
+    "qxt_ggml_q4_0_q8_0_tiled_linear": (c_int, [_P, _SZ, _P, _SZ, _U, _P, _SZ, _P, _SZ, _P, _SZ, _U, _U, _U, _P]),
     "qxt_q4_0_batch_prepare": (c_int, [POINTER(Q4Task), _U, POINTER(c_void_p)]),
     "qxt_q4_0_batch_launch": (c_int, [_P, _P]),
     "qxt_q4_0_batch_work_items": (_U, [_P]),

@@ -15,8 +15,19 @@ def ptr(t: torch.Tensor | None) -> ctypes.c_void_p | None:
 
 
 def row_stride(t: torch.Tensor) -> int:
-    """Byte distance between consecutive rows (dimension 0)."""
-    return int(t.stride(0)) * t.element_size()
+    """Byte distance between consecutive rows (dimension 0).
+
+    A tensor with a single row may carry any stride for dimension 0 (torch and
+    NumPy report 1 for transposed single-row views); its dense row length is
+    the stride then, which is what the C ABI's stride checks expect.
+    """
+    stride = int(t.stride(0))
+    if t.dim() >= 2 and t.shape[0] == 1:
+        row = 1
+        for extent in t.shape[1:]:
+            row *= int(extent)
+        stride = max(stride, row)
+    return stride * t.element_size()
 
 
 def rows_are_dense(t: torch.Tensor) -> bool:

@@ -20,7 +20,7 @@ from typing import Any
 import torch
 
 from qpu_xla_amd import _lib
-from qpu_xla_amd._tensors import ptr, require_gpu, row_stride, rows_are_dense, stream_handle
+from qpu_xla_amd._tensors import PACKED_WORD_DTYPES, ptr, require_gpu, row_stride, rows_are_dense, stream_handle
 from qpu_xla_amd.errors import KernelError
 from qpu_xla_amd.kernel import Kernel
 
@@ -29,6 +29,7 @@ Q4_0_BLOCK_BYTES = 18
 Q8_0_BLOCK_BYTES = 34
 OUTPUT_TILE = 16
 ROW_TILE = 4
+MX_ROW_TILE = 16  # row tile of the tiled (prefill) kernel's grid, as the reference's
 
 
 # ----------------------------------------------------------------- block codec
@@ -205,6 +206,125 @@ def ggml_q4_0_q8_0_block_dots(
         rows, blocks, weight_column_start, column_count, stream_handle(stream),
     )
     return dots
+
+
+# ------------------------------------------------------- tiled (prefill) layout
+# The split operands of the reference's GGML_Q4_0_Q8_0_TILED_LINEAR_KERNEL
+# (ggml_q4_0.py:844-967): activation int8 [M, K] + fp16 scale bits [M, B]
+# (2-byte halves, or 4-byte words when the reference's activation_scale_word
+# program is used); weight uint32 words [B * 8, N] of signed int8 quads + fp16
+# scale bits [B, N].  Word dtypes: int32/uint32; half dtypes: int16/uint16.
+
+_HALF_DTYPES = (torch.int16, torch.uint16)
+
+
+def pack_ggml_q4_0_tiled_weights(blocks: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Native Q4_0 weights uint8 [N, B, 18] -> (scale bits int16 [B, N], words int32 [B * 8, N]).
+
+    Same layout as the reference's ``pack_ggml_q4_0_tiled_weights``
+    (ggml_q4_0.py:844-855): word ``(8 b + g, n)`` holds the signed values
+    ``code - 8`` of elements ``4 g .. 4 g + 3`` of block ``b`` of output ``n``.
+    """
+    if blocks.dtype != torch.uint8 or blocks.dim() != 3 or blocks.shape[2] != Q4_0_BLOCK_BYTES:
+        raise ValueError("native Q4_0 weights must be uint8 [outputs, blocks, 18]")
+    outputs, nblocks, _ = blocks.shape
+    scale_bits = blocks[..., 0:2].contiguous().view(torch.int16).reshape(outputs, nblocks).t().contiguous()
+    qs = blocks[..., 2:]
+    values = torch.cat(((qs & 0x0F).to(torch.int8) - 8, (qs >> 4).to(torch.int8) - 8), dim=-1)
+    groups = values.reshape(outputs, nblocks, 8, 4).permute(1, 2, 0, 3).contiguous()
+    return scale_bits, groups.view(torch.int32).reshape(nblocks * 8, outputs)
+
+
+def split_ggml_q8_0_blocks(blocks: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Native Q8_0 activations uint8 [M, B, 34] -> (scale bits int16 [M, B], values uint8 [M, B * 32])."""
+    if blocks.dtype != torch.uint8 or blocks.dim() != 3 or blocks.shape[2] != Q8_0_BLOCK_BYTES:
+        raise ValueError("native Q8_0 activations must be uint8 [rows, blocks, 34]")
+    rows, nblocks, _ = blocks.shape
+    scales = blocks[..., 0:2].contiguous().view(torch.int16).reshape(rows, nblocks)
+    values = blocks[..., 2:].contiguous().reshape(rows, nblocks * Q4_0_BLOCK_ELEMENTS)
+    return scales, values
+
+
+def supports_ggml_q4_0_q8_0_tiled_linear(
+    activation_q: torch.Tensor,
+    activation_scales: torch.Tensor,
+    weight_q: torch.Tensor,
+    weight_scales: torch.Tensor,
+    destination: torch.Tensor,
+) -> bool:
+    """Whether split tensors meet the tiled contract (ggml_q4_0.py:886-920), widened to any M and N."""
+    tensors = (activation_q, activation_scales, weight_q, weight_scales, destination)
+    if not all(isinstance(t, torch.Tensor) and t.dim() == 2 for t in tensors):
+        return False
+    if any(t.device.type != "cuda" for t in tensors) or len({t.device for t in tensors}) != 1:
+        return False
+    if activation_q.dtype not in (torch.uint8, torch.int8) or weight_q.dtype not in PACKED_WORD_DTYPES:
+        return False
+    if activation_scales.dtype not in _HALF_DTYPES + PACKED_WORD_DTYPES or weight_scales.dtype not in _HALF_DTYPES:
+        return False
+    if destination.dtype != torch.float32:
+        return False
+    rows, columns = activation_q.shape
+    if rows <= 0 or columns <= 0 or columns % Q4_0_BLOCK_ELEMENTS:
+        return False
+    blocks = columns // Q4_0_BLOCK_ELEMENTS
+    outputs = weight_q.shape[1]
+    shapes_ok = (
+        outputs > 0
+        and tuple(activation_scales.shape) == (rows, blocks)
+        and tuple(weight_q.shape) == (blocks * 8, outputs)
+        and tuple(weight_scales.shape) == (blocks, outputs)
+        and tuple(destination.shape) == (rows, outputs)
+    )
+    return shapes_ok and all(t.is_contiguous() for t in tensors)
+
+
+def tiled_grid(rows: int, outputs: int) -> tuple[int, int, int]:
+    return ((outputs + OUTPUT_TILE - 1) // OUTPUT_TILE, (rows + MX_ROW_TILE - 1) // MX_ROW_TILE, 1)
+
+
+def _launch_tiled(activation_q, activation_scales, weight_q, weight_scales, destination, stream) -> None:
+    rows, columns = activation_q.shape
+    _lib.call(
+        "qxt_ggml_q4_0_q8_0_tiled_linear",
+        ptr(activation_q), row_stride(activation_q), ptr(activation_scales), row_stride(activation_scales),
+        activation_scales.element_size(), ptr(weight_q), row_stride(weight_q), ptr(weight_scales),
+        row_stride(weight_scales), ptr(destination), row_stride(destination),
+        rows, columns // Q4_0_BLOCK_ELEMENTS, weight_q.shape[1], stream_handle(stream),
+    )
+
+
+def _execute_ggml_q4_0_q8_0_tiled_linear(stream: Any, args: tuple[Any, ...], grid: tuple[int, int, int]) -> None:
+    if len(args) != 5 or not all(isinstance(a, torch.Tensor) for a in args):
+        raise KernelError("tiled Q4_0 linear expects split activation/weight scales, values, and output")
+    if not supports_ggml_q4_0_q8_0_tiled_linear(*args):
+        raise KernelError("tiled Q4_0 linear requires aligned contiguous split tensors")
+    activation_q, _, weight_q, _, destination = args
+    want = tiled_grid(activation_q.shape[0], weight_q.shape[1])
+    if tuple(grid) != want:
+        raise KernelError(f"tiled Q4_0 linear grid must be {want}, got {tuple(grid)}")
+    _launch_tiled(*args, stream)
+
+
+GGML_Q4_0_Q8_0_TILED_LINEAR_KERNEL = Kernel("gfx950.ggml_q4_0_q8_0_tiled_linear", _execute_ggml_q4_0_q8_0_tiled_linear)
+
+
+def ggml_q4_0_q8_0_tiled_linear(
+    activation_q: torch.Tensor,
+    activation_scales: torch.Tensor,
+    weight_q: torch.Tensor,
+    weight_scales: torch.Tensor,
+    destination: torch.Tensor | None = None,
+    *,
+    stream: Any = None,
+) -> torch.Tensor:
+    """Functional form of the tiled linear; returns the fp32 [M, N] destination."""
+    if destination is None:
+        destination = torch.empty((activation_q.shape[0], weight_q.shape[1]), dtype=torch.float32, device=weight_q.device)
+    if not supports_ggml_q4_0_q8_0_tiled_linear(activation_q, activation_scales, weight_q, weight_scales, destination):
+        raise ValueError("ggml_q4_0_q8_0_tiled_linear: operands do not meet the tiled layout contract")
+    _launch_tiled(activation_q, activation_scales, weight_q, weight_scales, destination, stream)
+    return destination
 
 
 class Q4_0LinearBatch:

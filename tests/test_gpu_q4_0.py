@@ -261,3 +261,71 @@ def test_batch_rejects_unsupported_tasks_and_injected_allocation_failure() -> No
         assert info.value.status == _lib.ALLOCATION_FAILED
     finally:
         _lib.set_failure_mask(_lib.FAIL_NONE)
+
+
+# ------------------------------------------------------------ tiled / prefill
+
+
+def _split_case(seed: int, rows: int, blocks: int, outputs: int):
+    rng = np.random.default_rng(seed)
+    act = oracle.pack_q8_0_blocks(
+        rng.uniform(0.001, 0.2, (rows, blocks)).astype(np.float16), rng.integers(-127, 128, (rows, blocks, 32))
+    )
+    wt = oracle.pack_q4_0_blocks(
+        rng.uniform(-0.2, 0.2, (outputs, blocks)).astype(np.float16), rng.integers(0, 16, (outputs, blocks, 32))
+    )
+    return act, wt
+
+
+@pytest.mark.parametrize("blocks", [1, 2])
+@pytest.mark.parametrize("scale_mode", ["fp16", "word"])
+def test_tiled_linear_reference_case_bit_exact(blocks: int, scale_mode: str) -> None:
+    # Inputs of tests/test_qpu_xla_ggml_q4_0.py:164-229 (seed 4480 + blocks, 16 x 16);
+    # the reference checks its QPU program within rtol 2e-6, this kernel is bit-exact.
+    rng = np.random.default_rng(4480 + blocks)
+    rows = outputs = 16
+    act = oracle.pack_q8_0_blocks(
+        rng.uniform(0.001, 0.2, (rows, blocks)).astype(np.float16), rng.integers(-127, 128, (rows, blocks, 32))
+    )
+    wt = oracle.pack_q4_0_blocks(
+        rng.uniform(-0.2, 0.2, (outputs, blocks)).astype(np.float16), rng.integers(0, 16, (outputs, blocks, 32))
+    )
+    expected = oracle.q4_0_q8_0_reference(act, wt)
+    scales, quants = oracle.split_q8_0_blocks(act)
+    if scale_mode == "word":
+        scales = scales.astype(np.uint32).view(np.int32)
+    else:
+        scales = scales.view(np.int16)
+    wscales, wquants = oracle.pack_q4_0_tiled_weights(wt)
+    destination = torch.full((rows, outputs), float("nan"), device="cuda")
+    args = (dev(quants), dev(scales), dev(wquants.view(np.int32)), dev(wscales.view(np.int16)), destination)
+    with Queue() as queue:
+        queue.submit(q4.GGML_Q4_0_Q8_0_TILED_LINEAR_KERNEL, args, grid=q4.tiled_grid(rows, outputs)).wait()
+    np.testing.assert_array_equal(destination.cpu().numpy(), expected)
+
+
+@pytest.mark.parametrize("rows,blocks,outputs", [(16, 2, 768), (17, 3, 40), (64, 5, 64), (130, 32, 300), (128, 64, 512)])
+def test_tiled_linear_shapes_bit_exact_and_device_packing(rows: int, blocks: int, outputs: int) -> None:
+    act, wt = _split_case(4488 + rows, rows, blocks, outputs)
+    expected = oracle.q4_0_q8_0_reference(act, wt)
+    wscales, wquants = q4.pack_ggml_q4_0_tiled_weights(dev(wt))
+    ref_scales, ref_quants = oracle.pack_q4_0_tiled_weights(wt)
+    np.testing.assert_array_equal(wscales.cpu().numpy().view(np.uint16), ref_scales)
+    np.testing.assert_array_equal(wquants.cpu().numpy().view(np.uint32), ref_quants)
+    ascales, aquants = q4.split_ggml_q8_0_blocks(dev(act))
+    out = q4.ggml_q4_0_q8_0_tiled_linear(aquants, ascales, wquants, wscales).cpu().numpy()
+    np.testing.assert_array_equal(out, expected)
+
+
+@pytest.mark.parametrize("rows,blocks,wcol0,ncols", [(16, 8, 0, 48), (33, 5, 3, 61), (100, 12, 0, 128), (64, 1, 16, 16)])
+def test_native_linear_prefill_rows_run_on_matrix_cores_bit_exact(rows: int, blocks: int, wcol0: int, ncols: int) -> None:
+    # rows >= 16 through the native-layout entry point: odd block counts give
+    # activation rows that are not 4-byte aligned; a column partition with a
+    # sentinel prefix checks that only the requested columns are written.
+    act, wt = _split_case(5000 + rows + blocks, rows, blocks, wcol0 + ncols + 5)
+    destination = torch.full((rows, ncols + 16), float(SENTINEL), device="cuda")
+    q4.ggml_q4_0_q8_0_linear(dev(act), dev(wt), destination, weight_column_start=wcol0,
+                             output_column_start=16, column_count=ncols)
+    out = destination.cpu().numpy()
+    np.testing.assert_array_equal(out[:, :16], SENTINEL)
+    np.testing.assert_array_equal(out[:, 16:], oracle.q4_0_q8_0_reference(act, wt[wcol0:wcol0 + ncols]))

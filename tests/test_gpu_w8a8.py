@@ -96,6 +96,33 @@ def test_streaming_kernel_fused_epilogue_on_edge_tiles_bit_exact() -> None:
     np.testing.assert_array_equal(out[rows], expected)
 
 
+@pytest.mark.parametrize("m,n,k", [(1, 16, 16), (1, 33, 48), (2, 100, 4096), (3, 4096, 2048), (4, 17, 1040),
+                                   (1, 14336, 4096), (1, 4096, 14336), (4, 64, 14336)])
+def test_gemv_rows_exact_both_layouts_and_epilogue(m: int, n: int, k: int) -> None:
+    # M <= 4 runs the dot4 GEMV kernels (weight [N, K] or packed K4 [K/4, N]).
+    rng = np.random.default_rng(m * 1000 + n + k)
+    a = rng.integers(-127, 128, size=(m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    expected = oracle.int8_gemm_i32(a, w)
+    np.testing.assert_array_equal(gemm_int8.w8a8_gemm_i32(dev(a), dev(w)).cpu().numpy(), expected)
+    if n % 4 == 0:
+        left, right = oracle.pack_int8_gemm_operands(a, np.ascontiguousarray(w.T))
+        out = torch.empty((m, n), dtype=torch.int32, device="cuda")
+        from qpu_xla_amd import _lib
+        from qpu_xla_amd._tensors import ptr, row_stride
+
+        lw, rw = words(left), words(right)
+        _lib.call("qxt_w8a8_gemm_i32", ptr(lw), row_stride(lw), ptr(rw), row_stride(rw), ptr(out), row_stride(out),
+                  m, n, k, _lib.WEIGHT_K4N, None)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(out.cpu().numpy(), expected)
+    sa = rng.uniform(0.001, 0.1, m).astype(np.float32)
+    sw = rng.uniform(0.001, 0.1, n).astype(np.float32)
+    bias = rng.standard_normal(n, dtype=np.float32)
+    y = gemm_int8.w8a8_gemm_dequantize(dev(a), dev(w), dev(sa), dev(sw), dev(bias)).cpu().numpy()
+    np.testing.assert_array_equal(y, oracle.dequantize_epilogue(expected, sa, sw, bias))
+
+
 def test_large_tile_gemm_over_several_rounds_with_edge_tile_exact() -> None:
     # 16 x 56 tiles of 256 x 256 (several rounds on a 256-CU device), the last
     # column of tiles partial; int32 accumulators and the fused epilogue.

@@ -169,3 +169,36 @@ def test_q4_0_quantiser_invariants_parity_unpinned_vs_ggml() -> None:
     # All-zero block: d = -0.0 (fp16 0x8000) and every code 8, as ggml's rule gives.
     assert blocks[3, 0, 0] == 0x00 and blocks[3, 0, 1] == 0x80
     np.testing.assert_array_equal(codes[3, 0], 8)
+
+
+def test_tiled_weight_words_hold_element_quads_of_each_block() -> None:
+    # Layout of pack_ggml_q4_0_tiled_weights (reference ggml_q4_0.py:844-855),
+    # checked element by element against the native block bytes.
+    rng = np.random.default_rng(11)
+    outputs, blocks = 5, 3
+    scales = rng.uniform(-1, 1, size=(outputs, blocks)).astype(np.float16)
+    codes = rng.integers(0, 16, size=(outputs, blocks, 32), dtype=np.uint8)
+    native = oracle.pack_q4_0_blocks(scales, codes)
+    scale_bits, words = oracle.pack_q4_0_tiled_weights(native)
+    assert scale_bits.dtype == np.uint16 and scale_bits.shape == (blocks, outputs)
+    assert words.dtype == np.uint32 and words.shape == (blocks * 8, outputs)
+    for n in range(outputs):
+        for b in range(blocks):
+            assert int(scale_bits[b, n]) == int(native[n, b, 0]) | (int(native[n, b, 1]) << 8)
+            for g in range(8):
+                word = int(words[b * 8 + g, n])
+                for i in range(4):
+                    byte = (word >> (8 * i)) & 0xFF
+                    signed = byte - 256 if byte > 127 else byte
+                    assert signed == int(codes[n, b, 4 * g + i]) - 8
+
+
+def test_split_q8_0_blocks_inverts_packing() -> None:
+    rng = np.random.default_rng(12)
+    scales = rng.uniform(0.001, 0.2, size=(4, 6)).astype(np.float16)
+    values = rng.integers(-128, 128, size=(4, 6, 32))
+    native = oracle.pack_q8_0_blocks(scales, values)
+    scale_bits, q = oracle.split_q8_0_blocks(native)
+    assert q.shape == (4, 192)
+    np.testing.assert_array_equal(scale_bits.view(np.float16), scales)
+    np.testing.assert_array_equal(q.view(np.int8).reshape(4, 6, 32), values.astype(np.int8))
