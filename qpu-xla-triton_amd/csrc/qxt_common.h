@@ -82,6 +82,33 @@ __device__ __forceinline__ uint32_t float_to_half_bits(float value) {
     return raw.x;
 }
 
+// Per-row int8 quantisation rule (PreparedW8A8Linear._prepare_values,
+// src/qpu_xla/models/tinyllama/quantization.py:156-171): scale =
+// max(fl32(absmax / 127), fl32(1/127)) (the floor is optional), q =
+// clip(rint(x / scale), +-127) with true division.  Shared by the
+// standalone quantiser and the GEMV kernels that quantise in place.
+__device__ __forceinline__ int clamp127(float r) {
+    int q = static_cast<int>(r);
+    return q < -127 ? -127 : (q > 127 ? 127 : q);
+}
+
+__device__ __forceinline__ float row_scale(float amax, bool floor) {
+    float s = amax / 127.0f;
+    // fl32(1/127) rounded from the double quotient, as np.float32(1.0 / 127.0).
+    if (floor) s = fmaxf(s, static_cast<float>(1.0 / 127.0));
+    return s;
+}
+
+__device__ __forceinline__ int quant_div(float v, float s) {
+    // True IEEE division (no reciprocal shortcut): x / scale, then rint.
+    return s > 0.0f ? clamp127(rintf(v / s)) : 0;
+}
+
+__device__ __forceinline__ uint32_t pack_bytes(int q0, int q1, int q2, int q3) {
+    return (static_cast<uint32_t>(q0) & 0xFFu) | ((static_cast<uint32_t>(q1) & 0xFFu) << 8) |
+           ((static_cast<uint32_t>(q2) & 0xFFu) << 16) | ((static_cast<uint32_t>(q3) & 0xFFu) << 24);
+}
+
 // Signed 4 x int8 dot product accumulated into int32 (v_dot4_i32_i8).
 __device__ __forceinline__ int dot4(int a, int b, int c) {
     return __builtin_amdgcn_sdot4(a, b, c, false);

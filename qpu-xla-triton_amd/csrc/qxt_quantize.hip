@@ -27,16 +27,6 @@ __device__ __forceinline__ float group8_max(float v) {
     return v;
 }
 
-__device__ __forceinline__ int clamp127(float r) {
-    int q = static_cast<int>(r);
-    return q < -127 ? -127 : (q > 127 ? 127 : q);
-}
-
-__device__ __forceinline__ uint32_t pack_bytes(int q0, int q1, int q2, int q3) {
-    return (static_cast<uint32_t>(q0) & 0xFFu) | ((static_cast<uint32_t>(q1) & 0xFFu) << 8) |
-           ((static_cast<uint32_t>(q2) & 0xFFu) << 16) | ((static_cast<uint32_t>(q3) & 0xFFu) << 24);
-}
-
 // Store a 32-bit word at a 2-byte-aligned address as two halves.
 __device__ __forceinline__ void store_u32_at_even(uint8_t *p, uint32_t word) {
     uint16_t *h = reinterpret_cast<uint16_t *>(p);
@@ -95,18 +85,6 @@ __device__ __forceinline__ float block_max(float v, float *scratch) {
     v = scratch[0];
     for (int w = 1; w < kThreads / 64; ++w) v = fmaxf(v, scratch[w]);
     return v;
-}
-
-__device__ __forceinline__ float row_scale(float amax, bool floor) {
-    float s = amax / 127.0f;
-    // fl32(1/127) rounded from the double quotient, as np.float32(1.0 / 127.0).
-    if (floor) s = fmaxf(s, static_cast<float>(1.0 / 127.0));
-    return s;
-}
-
-__device__ __forceinline__ int quant_div(float v, float s) {
-    // True IEEE division (no reciprocal shortcut): x / scale, then rint.
-    return s > 0.0f ? clamp127(rintf(v / s)) : 0;
 }
 
 // NV > 0: the row (columns % 4 == 0, <= 1024 * NV columns) is held in registers.

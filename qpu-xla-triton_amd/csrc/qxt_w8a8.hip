@@ -595,39 +595,110 @@ __device__ __forceinline__ int wave_sum(int v) {
 }
 
 template <int EPI>
-__device__ __forceinline__ void store_one(const GemmArgs &args, int row, int col, int acc) {
+__device__ __forceinline__ void store_one(const GemmArgs &args, int row, int col, int acc, float sa_row) {
     if constexpr (EPI == EPI_I32) {
         reinterpret_cast<int32_t *>(reinterpret_cast<uint8_t *>(args.acc) + static_cast<size_t>(row) * args.ldacc)[col] =
             acc;
     } else {
-        float y = static_cast<float>(acc) * args.sa[row];
+        float y = static_cast<float>(acc) * sa_row;
         y = y * args.sw[col];
         if constexpr (EPI == EPI_DEQUANT_BIAS) y = y + args.bias[col];
         reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(args.y) + static_cast<size_t>(row) * args.ldy)[col] = y;
     }
 }
 
-// Stage activation rows [0, MR) (zeros past M) as 16-byte chunks in LDS.
-template <int MR>
-__device__ __forceinline__ void stage_rows(const GemmArgs &args, v4u *act) {
+// fp32 activation rows quantised inside the GEMV workgroup (the dynamic
+// W8A8 linear at M <= 4): same rule as qxt_quantize_rows_int8, computed by
+// every workgroup; workgroup 0 also writes the int8 rows and scales to the
+// caller's workspaces (args.a / args.sa), as the two-kernel path does.
+// fp32 chunks of 16 bytes per thread that hold a whole quantised row: the
+// fused path runs for K <= 16384.
+constexpr int kGemvRowChunks = 16;
+
+struct FusedRows {
+    const float *x;
+    uint32_t ldx;     // bytes
+    uint32_t x_bytes; // descriptor range
+    int floor;
+};
+
+// Stage activation rows [0, MR) (zeros past M) as 16-byte chunks in LDS;
+// `row_sa` receives each row's scale (1 for stored int8 rows, whose scales
+// the epilogue reads from args.sa).
+template <int MR, bool FUSED>
+__device__ __forceinline__ void stage_rows(const GemmArgs &args, const FusedRows &f, v4u *act, float *row_sa,
+                                           float *scratch) {
     const int k16 = args.k / 16;
-    const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(args.a, args.a_bytes);
-    for (int i = threadIdx.x; i < MR * k16; i += kThreads) {
-        const int r = i / k16, c = i - r * k16;
-        const uint32_t off = r < args.m ? static_cast<uint32_t>(r) * args.lda + c * 16 : kOutOfRange;
-        act[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
+    if constexpr (!FUSED) {
+        const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(args.a, args.a_bytes);
+        for (int i = threadIdx.x; i < MR * k16; i += kThreads) {
+            const int r = i / k16, c = i - r * k16;
+            const uint32_t off = r < args.m ? static_cast<uint32_t>(r) * args.lda + c * 16 : kOutOfRange;
+            act[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
+        }
+        if (threadIdx.x < MR)
+            row_sa[threadIdx.x] = (args.sa != nullptr && threadIdx.x < args.m) ? args.sa[threadIdx.x] : 0.0f;
+    } else {
+        const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(f.x, f.x_bytes);
+        uint32_t *aw = reinterpret_cast<uint32_t *>(act);
+        const int k4 = args.k / 4;
+        for (int r = 0; r < MR; ++r) {
+            if (r >= args.m) {
+                for (int c = threadIdx.x; c < k4; c += kThreads) aw[r * k4 + c] = 0;
+                continue;
+            }
+            const uint32_t base = static_cast<uint32_t>(r) * f.ldx;
+            // The row is read once into registers (K <= 16384 here: at most
+            // 16 x 16 bytes per thread), reduced, then quantised from them.
+            v4u xv[kGemvRowChunks];
+            float amax = 0.0f;
+#pragma unroll
+            for (int u = 0; u < kGemvRowChunks; ++u) {
+                const int c = threadIdx.x + u * kThreads;
+                xv[u] = __builtin_amdgcn_raw_buffer_load_b128(rx, c < k4 ? base + c * 16 : kOutOfRange, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < kGemvRowChunks; ++u)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fabsf(__uint_as_float(xv[u][e])));
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+            if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = amax;
+            __syncthreads();
+            amax = fmaxf(fmaxf(scratch[0], scratch[1]), fmaxf(scratch[2], scratch[3]));
+            __syncthreads();  // scratch is reused by the next row
+            const float sc = row_scale(amax, f.floor != 0);
+#pragma unroll
+            for (int u = 0; u < kGemvRowChunks; ++u) {
+                const int c = threadIdx.x + u * kThreads;
+                if (c >= k4) break;
+                const v4u v = xv[u];
+                const uint32_t word = pack_bytes(quant_div(__uint_as_float(v[0]), sc), quant_div(__uint_as_float(v[1]), sc),
+                                                 quant_div(__uint_as_float(v[2]), sc), quant_div(__uint_as_float(v[3]), sc));
+                aw[r * k4 + c] = word;
+                if (blockIdx.x == 0)
+                    reinterpret_cast<uint32_t *>(const_cast<int8_t *>(args.a) + static_cast<size_t>(r) * args.lda)[c] = word;
+            }
+            if (threadIdx.x == 0) {
+                row_sa[r] = sc;
+                if (blockIdx.x == 0) const_cast<float *>(args.sa)[r] = sc;
+            }
+        }
     }
     __syncthreads();
 }
 
 // Weight [N, K] (K contiguous): each wave owns 4 output columns and streams
 // their K bytes 1 KB per load instruction (lane l takes bytes 16 l .. 16 l + 15
-// of each kilobyte), then reduces across the wave.
+// of each kilobyte), four kilobytes ahead of the one being reduced, the
+// first four requested before the activation is staged.  A wave sum per
+// column ends it.
 constexpr int kGemvColsNK = 16;  // per workgroup: 4 waves x 4 columns
-template <int MR, int EPI>
-__global__ __launch_bounds__(kThreads) void w8a8_gemv_nk_kernel(GemmArgs args) {
+template <int MR, int EPI, bool FUSED>
+__global__ __launch_bounds__(kThreads) void w8a8_gemv_nk_kernel(GemmArgs args, FusedRows f) {
     extern __shared__ v4u act[];  // [MR][K / 16]
-    stage_rows<MR>(args, act);
+    __shared__ float row_sa[4];
+    __shared__ float scratch[kThreads / 64];
     const int k16 = args.k / 16;
     const int lane = threadIdx.x & 63;
     const int n0 = blockIdx.x * kGemvColsNK + (threadIdx.x >> 6) * 4;
@@ -635,30 +706,44 @@ __global__ __launch_bounds__(kThreads) void w8a8_gemv_nk_kernel(GemmArgs args) {
     uint32_t row_off[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) row_off[j] = n0 + j < args.n ? static_cast<uint32_t>(n0 + j) * args.ldw : kOutOfRange;
+    auto load_cols = [&](v4u (&v)[4], int c) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            v[j] = __builtin_amdgcn_raw_buffer_load_b128(
+                rb, row_off[j] == kOutOfRange || c >= k16 ? kOutOfRange : row_off[j] + c * 16, 0, 0);
+    };
+    // Four kilobytes of every column in flight: ring slot d holds chunk
+    // c0 + 64 d of the current group of 256 chunks.
+    constexpr int kDepth = 4;
+    v4u ring[kDepth][4];
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) load_cols(ring[d], lane + 64 * d);
+    stage_rows<MR, FUSED>(args, f, act, row_sa, scratch);
     int acc[4][MR];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int r = 0; r < MR; ++r) acc[j][r] = 0;
-#pragma unroll 2
-    for (int c = lane; c < k16; c += 64) {
-        v4u wv[4];
+    for (int c0 = lane; c0 < k16; c0 += 64 * kDepth) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            wv[j] = __builtin_amdgcn_raw_buffer_load_b128(rb, row_off[j] == kOutOfRange ? kOutOfRange : row_off[j] + c * 16,
-                                                          0, 0);
+        for (int d = 0; d < kDepth; ++d) {
+            const int c = c0 + 64 * d;
+            if (c < k16) {
 #pragma unroll
-        for (int r = 0; r < MR; ++r) {
-            const v4u av = act[r * k16 + c];
+                for (int r = 0; r < MR; ++r) {
+                    const v4u av = act[r * k16 + c];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                int s = acc[j][r];
-                s = dot4(static_cast<int>(wv[j][0]), static_cast<int>(av[0]), s);
-                s = dot4(static_cast<int>(wv[j][1]), static_cast<int>(av[1]), s);
-                s = dot4(static_cast<int>(wv[j][2]), static_cast<int>(av[2]), s);
-                s = dot4(static_cast<int>(wv[j][3]), static_cast<int>(av[3]), s);
-                acc[j][r] = s;
+                    for (int j = 0; j < 4; ++j) {
+                        int sum = acc[j][r];
+                        sum = dot4(static_cast<int>(ring[d][j][0]), static_cast<int>(av[0]), sum);
+                        sum = dot4(static_cast<int>(ring[d][j][1]), static_cast<int>(av[1]), sum);
+                        sum = dot4(static_cast<int>(ring[d][j][2]), static_cast<int>(av[2]), sum);
+                        sum = dot4(static_cast<int>(ring[d][j][3]), static_cast<int>(av[3]), sum);
+                        acc[j][r] = sum;
+                    }
+                }
             }
+            load_cols(ring[d], c + 64 * kDepth);
         }
     }
 #pragma unroll
@@ -670,7 +755,7 @@ __global__ __launch_bounds__(kThreads) void w8a8_gemv_nk_kernel(GemmArgs args) {
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int r = 0; r < MR; ++r)
-                if (n0 + j < args.n && r < args.m) store_one<EPI>(args, r, n0 + j, acc[j][r]);
+                if (n0 + j < args.n && r < args.m) store_one<EPI>(args, r, n0 + j, acc[j][r], row_sa[r]);
     }
 }
 
@@ -678,11 +763,13 @@ __global__ __launch_bounds__(kThreads) void w8a8_gemv_nk_kernel(GemmArgs args) {
 // wave owns column n0 + l; the four waves split K and add their exact
 // partial sums through LDS.
 constexpr int kGemvColsK4N = 64;
-template <int MR, int EPI>
-__global__ __launch_bounds__(kThreads) void w8a8_gemv_k4n_kernel(GemmArgs args) {
+template <int MR, int EPI, bool FUSED>
+__global__ __launch_bounds__(kThreads) void w8a8_gemv_k4n_kernel(GemmArgs args, FusedRows f) {
     extern __shared__ v4u act[];  // [MR][K / 16]
     __shared__ int part[4][MR][64];
-    stage_rows<MR>(args, act);
+    __shared__ float row_sa[4];
+    __shared__ float scratch[kThreads / 64];
+    stage_rows<MR, FUSED>(args, f, act, row_sa, scratch);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = blockIdx.x * kGemvColsK4N + lane;
     const int k4 = args.k / 4;
@@ -708,7 +795,7 @@ __global__ __launch_bounds__(kThreads) void w8a8_gemv_k4n_kernel(GemmArgs args) 
 #pragma unroll
         for (int r = 0; r < MR; ++r) {
             const int s = part[0][r][lane] + part[1][r][lane] + part[2][r][lane] + part[3][r][lane];
-            if (r < args.m) store_one<EPI>(args, r, col, s);
+            if (r < args.m) store_one<EPI>(args, r, col, s, row_sa[r]);
         }
     }
 }
@@ -763,24 +850,33 @@ int launch_stream(const GemmArgs &args, int epi, hipStream_t stream) {
     return launch("w8a8_gemm_kernel", kernel, grid, dim3(kThreads), 0, stream, a2);
 }
 
-template <int MR>
-int launch_gemv(GemmArgs args, int epi, uint32_t layout, hipStream_t stream) {
+template <int MR, bool FUSED>
+int launch_gemv(GemmArgs args, const FusedRows &f, int epi, uint32_t layout, hipStream_t stream) {
     args.a_bytes = static_cast<uint32_t>(static_cast<size_t>(args.m - 1) * args.lda + args.k);
     const size_t lds = static_cast<size_t>(MR) * args.k;
     if (layout == QXT_W8A8_WEIGHT_K4N) {
         args.w_bytes = static_cast<uint32_t>(static_cast<size_t>(args.k / 4 - 1) * args.ldw + args.n * 4);
-        auto kernel = epi == EPI_I32        ? w8a8_gemv_k4n_kernel<MR, EPI_I32>
-                      : epi == EPI_DEQUANT ? w8a8_gemv_k4n_kernel<MR, EPI_DEQUANT>
-                                           : w8a8_gemv_k4n_kernel<MR, EPI_DEQUANT_BIAS>;
+        auto kernel = epi == EPI_I32        ? w8a8_gemv_k4n_kernel<MR, EPI_I32, FUSED>
+                      : epi == EPI_DEQUANT ? w8a8_gemv_k4n_kernel<MR, EPI_DEQUANT, FUSED>
+                                           : w8a8_gemv_k4n_kernel<MR, EPI_DEQUANT_BIAS, FUSED>;
         return launch("w8a8_gemv_kernel", kernel, dim3((args.n + kGemvColsK4N - 1) / kGemvColsK4N), dim3(kThreads), lds,
-                      stream, args);
+                      stream, args, f);
     }
     args.w_bytes = static_cast<uint32_t>(static_cast<size_t>(args.n - 1) * args.ldw + args.k);
-    auto kernel = epi == EPI_I32        ? w8a8_gemv_nk_kernel<MR, EPI_I32>
-                  : epi == EPI_DEQUANT ? w8a8_gemv_nk_kernel<MR, EPI_DEQUANT>
-                                       : w8a8_gemv_nk_kernel<MR, EPI_DEQUANT_BIAS>;
+    auto kernel = epi == EPI_I32        ? w8a8_gemv_nk_kernel<MR, EPI_I32, FUSED>
+                  : epi == EPI_DEQUANT ? w8a8_gemv_nk_kernel<MR, EPI_DEQUANT, FUSED>
+                                       : w8a8_gemv_nk_kernel<MR, EPI_DEQUANT_BIAS, FUSED>;
     return launch("w8a8_gemv_kernel", kernel, dim3((args.n + kGemvColsNK - 1) / kGemvColsNK), dim3(kThreads), lds,
-                  stream, args);
+                  stream, args, f);
+}
+
+template <bool FUSED>
+int dispatch_gemv(const GemmArgs &args, const FusedRows &f, int epi, uint32_t layout, hipStream_t stream) {
+    switch (args.m) {
+        case 1: return launch_gemv<1, FUSED>(args, f, epi, layout, stream);
+        case 2: return launch_gemv<2, FUSED>(args, f, epi, layout, stream);
+        default: return launch_gemv<4, FUSED>(args, f, epi, layout, stream);
+    }
 }
 
 // Rows up to which the GEMV path runs; its activation rows (padded to 1, 2
@@ -788,15 +884,13 @@ int launch_gemv(GemmArgs args, int epi, uint32_t layout, hipStream_t stream) {
 constexpr int kGemvMaxRows = 4;
 constexpr size_t kGemvMaxLds = 60 * 1024;
 
+bool gemv_path(int m, int k) {
+    const int rows = m <= 2 ? m : 4;
+    return m <= kGemvMaxRows && static_cast<size_t>(rows) * k <= kGemvMaxLds;
+}
+
 int run_gemm(const GemmArgs &args, int epi, uint32_t layout, hipStream_t stream) {
-    const int gemv_rows = args.m <= 2 ? args.m : 4;
-    if (args.m <= kGemvMaxRows && static_cast<size_t>(gemv_rows) * args.k <= kGemvMaxLds) {
-        switch (args.m) {
-            case 1: return launch_gemv<1>(args, epi, layout, stream);
-            case 2: return launch_gemv<2>(args, epi, layout, stream);
-            default: return launch_gemv<4>(args, epi, layout, stream);
-        }
-    }
+    if (gemv_path(args.m, args.k)) return dispatch_gemv<false>(args, FusedRows{}, epi, layout, stream);
     // 256 x 256 tiles once they give every CU a workgroup; 128 x 128 below that.
     const long cus = compute_units();
     const long tm = (args.m + 255) / 256, tn = (args.n + 255) / 256;
@@ -914,6 +1008,20 @@ int qxt_w8a8_linear(const float *x, size_t ldx, int8_t *qa, size_t ldqa, float *
     if (x == nullptr || ldx % 4 || ldx < static_cast<size_t>(k) * 4 || !aligned(x, 4))
         return fail(QXT_INVALID_ARGUMENT, "w8a8 linear: bad activation input");
     if (flags & ~QXT_QUANT_NO_SCALE_FLOOR) return fail(QXT_INVALID_ARGUMENT, "w8a8 linear: unknown flags");
+    if (gemv_path(static_cast<int>(m), static_cast<int>(k)) && k <= 4u * kThreads * kGemvRowChunks &&
+        aligned(x, 16) && ldx % 16 == 0 &&
+        static_cast<uint64_t>(m - 1) * ldx + static_cast<uint64_t>(k) * 4 < (1ull << 31)) {
+        // One launch: every GEMV workgroup quantises the rows itself.
+        rc = injected(QXT_FAIL_SUBMISSION);
+        if (rc != QXT_OK) return rc;
+        GemmArgs args{qa, ldqa, static_cast<const uint8_t *>(w), ldw, nullptr, 0, sa, column_scales, bias,
+                      y, ldy, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k)};
+        const FusedRows f{x, static_cast<uint32_t>(ldx),
+                          static_cast<uint32_t>(static_cast<uint64_t>(m - 1) * ldx + static_cast<uint64_t>(k) * 4),
+                          (flags & QXT_QUANT_NO_SCALE_FLOOR) ? 0 : 1};
+        return dispatch_gemv<true>(args, f, bias != nullptr ? EPI_DEQUANT_BIAS : EPI_DEQUANT, weight_layout,
+                                   as_stream(stream));
+    }
     rc = qxt_quantize_rows_int8(x, ldx, qa, ldqa, sa, m, k, k, flags, stream);
     if (rc != QXT_OK) return rc;
     GemmArgs args{qa, ldqa, static_cast<const uint8_t *>(w), ldw, nullptr, 0, sa, column_scales, bias,

@@ -123,6 +123,38 @@ def test_gemv_rows_exact_both_layouts_and_epilogue(m: int, n: int, k: int) -> No
     np.testing.assert_array_equal(y, oracle.dequantize_epilogue(expected, sa, sw, bias))
 
 
+@pytest.mark.parametrize("m,n,k", [(1, 16, 16), (1, 4096, 14336), (2, 100, 4096), (3, 33, 2048), (4, 14336, 4096)])
+@pytest.mark.parametrize("floor", [True, False])
+def test_small_m_linear_quantises_in_the_gemv_kernel_bit_exact(m: int, n: int, k: int, floor: bool) -> None:
+    # M <= 4: one launch quantises the rows inside every GEMV workgroup; the
+    # workspaces still receive the int8 rows and scales.
+    from qpu_xla_amd import _lib
+    from qpu_xla_amd._tensors import ptr, row_stride
+
+    rng = np.random.default_rng(7000 + m * 10 + k)
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    if k >= 64:
+        x[:, rng.choice(k, max(1, k // 1000), replace=False)] *= 20.0
+    x[0, :4] = [0.5, -0.5, 1.5, 2.5]
+    wf = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    qw, sw = oracle.quantize_per_output_channel_int8(wf)
+    bias = (rng.standard_normal(n, dtype=np.float32) * np.float32(0.1)).astype(np.float32)
+    xd = dev(x)
+    qa = torch.full((m, k), 99, dtype=torch.int8, device="cuda")
+    sa = torch.full((m,), -1.0, dtype=torch.float32, device="cuda")
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    w_d, sw_d, b_d = dev(qw), dev(sw), dev(bias)
+    flags = 0 if floor else _lib.QUANT_NO_SCALE_FLOOR
+    _lib.call("qxt_w8a8_linear", ptr(xd), row_stride(xd), ptr(qa), row_stride(qa), ptr(sa), ptr(w_d), row_stride(w_d),
+              ptr(sw_d), ptr(b_d), ptr(y), row_stride(y), m, n, k, _lib.WEIGHT_NK, flags, None)
+    torch.cuda.synchronize()
+    qa_ref, sa_ref = oracle.quantize_rows_int8(x, floor=floor)
+    np.testing.assert_array_equal(qa.cpu().numpy(), qa_ref)
+    np.testing.assert_array_equal(sa.cpu().numpy(), sa_ref)
+    expected = oracle.dequantize_epilogue(oracle.int8_gemm_i32(qa_ref, qw), sa_ref, sw, bias)
+    np.testing.assert_array_equal(y.cpu().numpy(), expected)
+
+
 def test_large_tile_gemm_over_several_rounds_with_edge_tile_exact() -> None:
     # 16 x 56 tiles of 256 x 256 (several rounds on a 256-CU device), the last
     # column of tiles partial; int32 accumulators and the fused epilogue.
