@@ -9,10 +9,16 @@ Host-side mirror of the reference's W8A8 contract owner,
   (``scale = max(absmax/127, 1/127)``, ``rint(w / scale)`` clipped to +-127),
   run by the per-row GPU quantiser;
 * ``w8a8_linear`` -- the whole dynamic operator (per-row activation
-  quantisation, int8 MFMA GEMM, fused dequant + bias) as two kernels;
-* ``PreparedW8A8Linear`` (``:57-330``) -- a persistent plan owning the
+  quantisation, int8 MFMA GEMM or dot4 GEMV, fused dequant + bias);
+* ``PreparedW8A8Linear`` (``:57-878``) -- a persistent plan owning the
   device weights and the activation workspace, bound to its first queue and
-  allowing one in-flight invocation, as the reference plan does.
+  allowing one in-flight invocation, as the reference plan does; its
+  partitioned ("hybrid") forms split rows or output columns between two
+  queues, both on the GPU;
+* ``CalibratedW8A8Linear`` (``:881-1082``) -- dispatches only measured
+  ``supported-win`` candidates of the exact shape class from a
+  ``CandidateRegistry``.  There is no CPU reference path: a shape without a
+  GPU or hybrid winner raises instead of running on the host.
 """
 
 from __future__ import annotations
@@ -24,8 +30,11 @@ import torch
 
 from qpu_xla_amd import _lib
 from qpu_xla_amd._tensors import ptr, require_gpu, row_stride, rows_are_dense, stream_handle
+from qpu_xla_amd.candidates import CandidateRecord, CandidateRegistry
 from qpu_xla_amd.errors import DependencyError
+from qpu_xla_amd.kernels.gemm_int8 import w8a8_gemm_dequantize
 from qpu_xla_amd.kernels.quantize import quantize_rows_int8
+from qpu_xla_amd.placement import Placement
 from qpu_xla_amd.queue import Event, Queue
 
 INT32_MAX = 2**31 - 1
@@ -114,15 +123,36 @@ def w8a8_linear(
     return out
 
 
+PARTITION_ALIGNMENT = 16
+LINEAR_OPERATION = "linear"
+W8A8_DTYPE = "w8a8-i32-fp32"
+# int8 [N, K] rows are byte-identical to the reference's packed-K4 words.
+W8A8_LAYOUT = "row-major-packed-k4"
+
+
+def w8a8_shape_class(batch: int, features: int, outputs: int) -> str:
+    """Shape-class key of a W8A8 linear record: ``"{M}x{K}x{N}"``."""
+    return f"{batch}x{features}x{outputs}"
+
+
 class PreparedW8A8Linear:
     """Persistent W8A8 projection plan on the GPU placement.
 
     Owns the weight (padded to a multiple of 16 along K, zero columns), an
     optional bias and the activation workspace for up to ``max_batch`` rows.
     ``execute`` quantises the fp32 source per row on the GPU and runs the
-    fused MFMA GEMM + dequant (+ bias) epilogue on the queue's stream.  The
-    plan binds to its first queue and allows one in-flight invocation
-    (``quantization.py:288-295``), because the workspace is reused.
+    int8 GEMM (dot4 GEMV for M <= 4) with the fused dequant (+ bias)
+    epilogue on the queue's stream.  The plan binds to its first queue and
+    allows one in-flight invocation (``quantization.py:288-295``), because
+    the workspace is reused.
+
+    ``execute_hybrid`` / ``execute_hybrid_rows`` keep the reference's
+    partition contract (``quantization.py:350-662``): an aligned prefix of
+    output columns or rows goes to ``qpu_queue`` and the disjoint tail to
+    ``cpu_queue``.  Here both queues are HIP streams of the same GPU -- the
+    tail is not computed on the host -- so each partition is exactly the
+    work one device of a sharded deployment would run; results are
+    bit-identical to ``execute``.
     """
 
     def __init__(self, weight: QuantizedMatrixInt8, *, max_batch: int, bias: torch.Tensor | None = None) -> None:
@@ -138,6 +168,7 @@ class PreparedW8A8Linear:
         device = weight.values.device
         if device.type != "cuda":
             raise ValueError("PreparedW8A8Linear requires weights on a HIP device (no CPU fallback)")
+        self.device = device
         values = torch.zeros((outputs, self.padded_features), dtype=torch.int8, device=device)
         values[:, :features] = weight.values
         self.weight = QuantizedMatrixInt8(values, weight.scales.contiguous())
@@ -148,6 +179,7 @@ class PreparedW8A8Linear:
         self._qa = torch.zeros((max_batch, self.padded_features), dtype=torch.int8, device=device)
         self._sa = torch.zeros((max_batch,), dtype=torch.float32, device=device)
         self._queue: Queue | None = None
+        self._second_queue: Queue | None = None
         self._last_event: Event | None = None
         self._closed = False
 
@@ -166,40 +198,371 @@ class PreparedW8A8Linear:
             self._last_event.wait()
         self._closed = True
 
-    def execute(self, destination: torch.Tensor, source: torch.Tensor, *, queue: Queue, wait_for=()) -> Event:
-        """Submit quantise + GEMM + epilogue; returns the completion event."""
+    @property
+    def activation_workspace(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """(int8 [max_batch, padded K], fp32 [max_batch]) read by ``execute_prepared``."""
+        return self._qa, self._sa
+
+    # ------------------------------------------------------------ validation
+
+    def _begin(self) -> None:
         if self._closed:
             raise RuntimeError("prepared W8A8 linear plan is closed")
         if self._last_event is not None and not self._last_event.done:
             raise RuntimeError("prepared W8A8 linear plan already has an in-flight invocation")
+
+    def _bind(self, queue: Queue, second: Queue | None = None) -> None:
+        if second is not None and second is queue:
+            raise DependencyError("hybrid W8A8 linear requires two distinct queues")
+        for q in (queue, second):
+            if q is not None and q.device != self.device:
+                raise DependencyError("prepared W8A8 linear queues must belong to the plan device")
         if self._queue is None:
             self._queue = queue
         elif self._queue is not queue:
             raise DependencyError("prepared W8A8 linear plan is bound to its first submission queue")
+        if second is not None:
+            if self._second_queue is None:
+                self._second_queue = second
+            elif self._second_queue is not second:
+                raise DependencyError("prepared W8A8 linear plan is bound to its first partition queue")
+
+    def _check_io(self, destination: torch.Tensor, source: torch.Tensor) -> int:
         if source.dtype != torch.float32 or destination.dtype != torch.float32:
             raise ValueError("prepared W8A8 linear requires float32 source and destination")
         if source.dim() != 2 or destination.dim() != 2:
             raise ValueError("prepared W8A8 linear requires rank-2 source and destination")
         batch, features = source.shape
-        if batch > self.max_batch or features != self.features:
+        if batch <= 0 or batch > self.max_batch or features != self.features:
             raise ValueError("prepared W8A8 linear source exceeds the plan shape")
         if tuple(destination.shape) != (batch, self.outputs):
             raise ValueError("prepared W8A8 linear destination shape does not align")
-        if source.device != self.weight.values.device or destination.device != self.weight.values.device:
+        if source.device != self.device or destination.device != self.device:
             raise DependencyError("prepared W8A8 linear tensors must live on the plan device")
+        return batch
+
+    def _staged(self, source: torch.Tensor) -> torch.Tensor:
+        """Source with padded K and dense rows (a copy into the plan buffer when needed).
+
+        Runs on the current stream; callers enter the queue's stream first.
+        """
+        if self.padded_features == self.features and rows_are_dense(source):
+            return source
+        staged = self._source[: source.shape[0]]
+        staged[:, : self.features].copy_(source)
+        return staged
+
+    @staticmethod
+    def _record(queue: Queue, name: str) -> Event:
+        hip_event = torch.cuda.Event()
+        hip_event.record(queue.stream)
+        return Event(queue, name, "gpu", hip_event)
+
+    # ------------------------------------------------------------- execution
+
+    def execute(self, destination: torch.Tensor, source: torch.Tensor, *, queue: Queue, wait_for=()) -> Event:
+        """Submit quantise + GEMM + epilogue; returns the completion event."""
+        self._begin()
+        self._bind(queue)
+        self._check_io(destination, source)
         queue._wait_dependencies(wait_for)
         with torch.cuda.stream(queue.stream):
-            if self.padded_features != features or not rows_are_dense(source):
-                staged = self._source[:batch]
-                staged[:, :features].copy_(source)
-                src = staged
-            else:
-                src = source
-            w8a8_linear(
-                src, self.weight, self.bias, destination,
-                workspace=(self._qa, self._sa), stream=queue,
-            )
-            hip_event = torch.cuda.Event()
-            hip_event.record(queue.stream)
-        self._last_event = Event(queue, "gfx950.w8a8_linear", "gpu", hip_event)
+            src = self._staged(source)
+            w8a8_linear(src, self.weight, self.bias, destination, workspace=(self._qa, self._sa), stream=queue)
+            self._last_event = self._record(queue, "gfx950.w8a8_linear")
         return self._last_event
+
+    def execute_prepared(self, destination: torch.Tensor, *, batch: int, queue: Queue, wait_for=()) -> Event:
+        """GEMM + epilogue over an activation already quantised into ``activation_workspace``.
+
+        Mirrors ``execute_prepared`` (``quantization.py:326-347``): an
+        enclosing stage wrote ``batch`` int8 rows (zero-padded to the padded
+        K) and their scales; ``wait_for`` orders this launch after it.
+        """
+        self._begin()
+        self._bind(queue)
+        if destination.dtype != torch.float32 or destination.dim() != 2:
+            raise ValueError("prepared W8A8 linear destination must be rank-2 float32")
+        if batch <= 0 or batch > self.max_batch or tuple(destination.shape) != (batch, self.outputs):
+            raise ValueError("prepared W8A8 linear destination shape does not align")
+        if destination.device != self.device:
+            raise DependencyError("prepared W8A8 linear destination must live on the plan device")
+        queue._wait_dependencies(wait_for)
+        with torch.cuda.stream(queue.stream):
+            w8a8_gemm_dequantize(
+                self._qa[:batch], self.weight.values, self._sa, self.weight.scales, self.bias, destination,
+                stream=queue,
+            )
+            self._last_event = self._record(queue, "gfx950.w8a8_gemm_dequantize")
+        return self._last_event
+
+    def execute_hybrid(
+        self,
+        destination: torch.Tensor,
+        source: torch.Tensor,
+        *,
+        qpu_queue: Queue,
+        cpu_queue: Queue,
+        qpu_outputs: int,
+        wait_for=(),
+    ) -> Event:
+        """Output columns [0, qpu_outputs) on ``qpu_queue``, the rest on ``cpu_queue`` (both GPU streams).
+
+        The activation is quantised once on ``qpu_queue``; the second queue
+        waits for it, then both run the fused GEMM over their column range.
+        The returned event (on ``qpu_queue``) completes after both.
+        """
+        self._begin()
+        batch = self._check_io(destination, source)
+        if qpu_outputs <= 0 or qpu_outputs >= self.outputs or qpu_outputs % PARTITION_ALIGNMENT:
+            raise ValueError("hybrid W8A8 qpu_outputs must be aligned and leave a non-empty tail")
+        self._bind(qpu_queue, cpu_queue)
+        qpu_queue._wait_dependencies(wait_for)
+        cpu_queue._wait_dependencies(wait_for)
+        split = int(qpu_outputs)
+        with torch.cuda.stream(qpu_queue.stream):
+            src = source
+            if not rows_are_dense(source):
+                src = self._source[:batch, : self.features]
+                src.copy_(source)
+            # The quantiser zero-fills the padded K columns of the workspace.
+            quantize_rows_int8(src, padded_columns=self.padded_features, out=self._qa, scales=self._sa, stream=qpu_queue)
+            quantized = self._record(qpu_queue, "gfx950.quantize_rows_int8")
+        cpu_queue._wait_dependencies((quantized,))
+        parts = ((qpu_queue, slice(0, split)), (cpu_queue, slice(split, self.outputs)))
+        for queue, cols in parts:
+            with torch.cuda.stream(queue.stream):
+                w8a8_gemm_dequantize(
+                    self._qa[:batch], self.weight.values[cols], self._sa, self.weight.scales[cols],
+                    None if self.bias is None else self.bias[cols], destination[:, cols], stream=queue,
+                )
+        tail = self._record(cpu_queue, "gfx950.w8a8_gemm_dequantize")
+        qpu_queue._wait_dependencies((tail,))
+        self._last_event = self._record(qpu_queue, "gfx950.w8a8_linear.hybrid_join")
+        return self._last_event
+
+    def execute_hybrid_rows(
+        self,
+        destination: torch.Tensor,
+        source: torch.Tensor,
+        *,
+        qpu_queue: Queue,
+        cpu_queue: Queue,
+        qpu_rows: int,
+        wait_for=(),
+    ) -> Event:
+        """Rows [0, qpu_rows) on ``qpu_queue``, the rest on ``cpu_queue`` (both GPU streams).
+
+        Per-row quantisation makes the row partitions independent: each
+        queue runs the whole operator on its rows with its own slice of the
+        workspace.  The returned event (on ``qpu_queue``) completes after both.
+        """
+        self._begin()
+        batch = self._check_io(destination, source)
+        if qpu_rows <= 0 or qpu_rows >= batch or qpu_rows % PARTITION_ALIGNMENT:
+            raise ValueError("hybrid W8A8 qpu_rows must be aligned and leave a non-empty tail")
+        self._bind(qpu_queue, cpu_queue)
+        qpu_queue._wait_dependencies(wait_for)
+        cpu_queue._wait_dependencies(wait_for)
+        split = int(qpu_rows)
+        with torch.cuda.stream(qpu_queue.stream):
+            src = self._staged(source)
+            if src is not source:
+                cpu_queue._wait_dependencies((self._record(qpu_queue, "gfx950.stage_source"),))
+        for queue, rows in ((qpu_queue, slice(0, split)), (cpu_queue, slice(split, batch))):
+            with torch.cuda.stream(queue.stream):
+                w8a8_linear(
+                    src[rows], self.weight, self.bias, destination[rows],
+                    workspace=(self._qa[rows], self._sa[rows]), stream=queue,
+                )
+        tail = self._record(cpu_queue, "gfx950.w8a8_linear")
+        qpu_queue._wait_dependencies((tail,))
+        self._last_event = self._record(qpu_queue, "gfx950.w8a8_linear.hybrid_join")
+        return self._last_event
+
+
+# --------------------------------------------------------- calibrated dispatch
+
+
+@dataclass(frozen=True)
+class W8A8Dispatch:
+    """Outcome of candidate selection: where one call runs and on which record."""
+
+    placement: Placement
+    record: CandidateRecord
+
+    @property
+    def axis(self) -> str | None:
+        return None if self.record.partition is None else self.record.partition.axis
+
+    @property
+    def units(self) -> int | None:
+        return None if self.record.partition is None else self.record.partition.qpu_units
+
+
+def _fastest(records: tuple[CandidateRecord, ...] | list[CandidateRecord]) -> CandidateRecord:
+    def median_seconds(record: CandidateRecord) -> float:
+        return float("inf") if record.performance is None else record.performance.candidate_median_seconds
+
+    return min(records, key=median_seconds)
+
+
+def select_w8a8_dispatch(
+    candidates: CandidateRegistry,
+    *,
+    batch: int,
+    features: int,
+    outputs: int,
+    placement: Placement = Placement.AUTO,
+    qpu_rows: int | None = None,
+    qpu_outputs: int | None = None,
+    partition_queue: bool = False,
+) -> W8A8Dispatch:
+    """Pick the exact-shape ``supported-win`` record a W8A8 call runs on.
+
+    Same rules as ``CalibratedW8A8Linear.execute`` (``quantization.py:966-1060``)
+    with the GPU in the accelerator's place: ``Placement.GPU`` needs a
+    ``"gpu"`` record, ``HYBRID`` a ``"hybrid"`` record whose partition matches
+    the requested axis/size and a second queue, ``AUTO`` takes the fastest
+    executable record by median candidate time.  ``"qpu"`` records are
+    VideoCore measurements and never run here.  Where the reference falls
+    back to its CPU reference, this raises ``ValueError``.
+    """
+    if qpu_rows is not None and qpu_outputs is not None:
+        raise ValueError("qpu_rows and qpu_outputs are mutually exclusive")
+    partitioned = qpu_rows is not None or qpu_outputs is not None
+    if placement in {Placement.CPU, Placement.QPU, Placement.GPU} and partitioned:
+        raise ValueError("hybrid partitions require HYBRID or AUTO placement")
+    if placement is Placement.CPU:
+        raise ValueError("the gfx950 library has no CPU placement for W8A8 linear; use GPU, HYBRID or AUTO")
+    if placement is Placement.QPU:
+        raise ValueError("the VideoCore QPU placement does not exist on gfx950; use Placement.GPU")
+    exact = candidates.supported_for(
+        operation=LINEAR_OPERATION, dtype=W8A8_DTYPE, layout=W8A8_LAYOUT,
+        shape_class=w8a8_shape_class(batch, features, outputs),
+    )
+    gpu_records = tuple(r for r in exact if r.placement == Placement.GPU.value)
+
+    def matches(record: CandidateRecord) -> bool:
+        part = record.partition
+        if part is None:
+            return False
+        if qpu_rows is not None:
+            return part.axis == "rows" and part.qpu_units == qpu_rows
+        if qpu_outputs is not None:
+            return part.axis == "outputs" and part.qpu_units == qpu_outputs
+        return part.axis in ("rows", "outputs")
+
+    hybrid_records = tuple(r for r in exact if r.placement == Placement.HYBRID.value and matches(r))
+    hybrid_ok = bool(hybrid_records) and partition_queue
+    if placement is Placement.GPU:
+        if not gpu_records:
+            raise ValueError("no measured supported-win W8A8 GPU candidate exists for this exact shape")
+        return W8A8Dispatch(Placement.GPU, _fastest(gpu_records))
+    if placement is Placement.HYBRID:
+        if not hybrid_ok:
+            raise ValueError("no executable supported-win W8A8 hybrid candidate exists for this exact shape")
+        return W8A8Dispatch(Placement.HYBRID, _fastest(hybrid_records))
+    if partitioned and not hybrid_ok:
+        raise ValueError("no supported W8A8 hybrid partition matches the requested axis and size")
+    executable = [*(() if partitioned else gpu_records), *(hybrid_records if hybrid_ok else ())]
+    if not executable:
+        raise ValueError(
+            f"no measured supported-win W8A8 GPU or hybrid candidate for shape "
+            f"{w8a8_shape_class(batch, features, outputs)}; this library has no CPU reference fallback"
+        )
+    record = _fastest(executable)
+    return W8A8Dispatch(Placement(record.placement), record)
+
+
+class CalibratedW8A8Linear:
+    """Dispatch a W8A8 linear only to measured GPU (or partitioned GPU) winners.
+
+    Mirrors ``CalibratedW8A8Linear`` (``quantization.py:881-1062``):
+    ``execute`` validates the call, picks the exact-shape winner with
+    ``select_w8a8_dispatch`` and runs it through a ``PreparedW8A8Linear``,
+    which is created only when the registry holds a GPU or hybrid winner for
+    some batch size up to ``max_batch``.
+    """
+
+    def __init__(
+        self,
+        weight: QuantizedMatrixInt8,
+        *,
+        max_batch: int,
+        candidates: CandidateRegistry,
+        bias: torch.Tensor | None = None,
+    ) -> None:
+        if max_batch <= 0:
+            raise ValueError("calibrated W8A8 linear max_batch must be positive")
+        self.weight = weight
+        self.max_batch = max_batch
+        self.candidates = candidates
+        outputs, features = weight.shape
+        wanted = {w8a8_shape_class(b, features, outputs) for b in range(1, max_batch + 1)}
+        executable = any(
+            r.placement in (Placement.GPU.value, Placement.HYBRID.value)
+            and (r.operation, r.dtype, r.layout) == (LINEAR_OPERATION, W8A8_DTYPE, W8A8_LAYOUT)
+            and r.shape_class in wanted
+            for r in candidates.supported
+        )
+        self._gpu = PreparedW8A8Linear(weight, max_batch=max_batch, bias=bias) if executable else None
+        self.last_dispatch: W8A8Dispatch | None = None
+        self._closed = False
+
+    def __enter__(self) -> "CalibratedW8A8Linear":
+        if self._closed:
+            raise RuntimeError("calibrated W8A8 linear is closed")
+        return self
+
+    def __exit__(self, *exc: object) -> None:
+        self.close()
+
+    def close(self) -> None:
+        if self._closed:
+            return
+        if self._gpu is not None:
+            self._gpu.close()
+        self._closed = True
+
+    def execute(
+        self,
+        destination: torch.Tensor,
+        source: torch.Tensor,
+        *,
+        queue: Queue,
+        cpu_queue: Queue | None = None,
+        placement: Placement = Placement.AUTO,
+        qpu_rows: int | None = None,
+        qpu_outputs: int | None = None,
+        wait_for=(),
+    ) -> Event:
+        """Run the exact-shape winner; ``cpu_queue`` is the second (GPU) queue of a partitioned run."""
+        if self._closed:
+            raise RuntimeError("calibrated W8A8 linear is closed")
+        if source.dtype != torch.float32 or destination.dtype != torch.float32:
+            raise ValueError("calibrated W8A8 linear requires FP32 source and destination")
+        if source.dim() != 2 or destination.dim() != 2:
+            raise ValueError("calibrated W8A8 linear requires rank-2 tensors")
+        outputs, features = self.weight.shape
+        batch = int(source.shape[0])
+        if batch > self.max_batch or int(source.shape[1]) != features:
+            raise ValueError("calibrated W8A8 source exceeds its planned shape")
+        if tuple(destination.shape) != (batch, outputs):
+            raise ValueError("calibrated W8A8 destination shape does not align")
+        dispatch = select_w8a8_dispatch(
+            self.candidates, batch=batch, features=features, outputs=outputs, placement=placement,
+            qpu_rows=qpu_rows, qpu_outputs=qpu_outputs, partition_queue=cpu_queue is not None,
+        )
+        assert self._gpu is not None  # a winner for this batch exists, so the plan was prepared
+        self.last_dispatch = dispatch
+        if dispatch.placement is Placement.GPU:
+            return self._gpu.execute(destination, source, queue=queue, wait_for=wait_for)
+        assert cpu_queue is not None and dispatch.units is not None
+        if dispatch.axis == "rows":
+            return self._gpu.execute_hybrid_rows(
+                destination, source, qpu_queue=queue, cpu_queue=cpu_queue, qpu_rows=dispatch.units, wait_for=wait_for,
+            )
+        return self._gpu.execute_hybrid(
+            destination, source, qpu_queue=queue, cpu_queue=cpu_queue, qpu_outputs=dispatch.units, wait_for=wait_for,
+        )

@@ -276,3 +276,104 @@ def test_prepared_plan_binds_queue_pads_k_and_matches_oracle() -> None:
             plan.execute(destination, dev(x), queue=other)
         with pytest.raises(ValueError):
             plan.execute(torch.empty((9, n), device="cuda"), dev(np.zeros((9, k), np.float32)), queue=queue)
+
+
+def _plan_case(seed: int, m: int, k: int, n: int):
+    rng = np.random.default_rng(seed)
+    w = rng.standard_normal((n, k), dtype=np.float32)
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    bias = rng.standard_normal(n, dtype=np.float32)
+    qw, sw = oracle.quantize_per_output_channel_int8(w)
+    return x, QuantizedMatrixInt8(dev(qw), dev(sw)), bias, oracle.w8a8_linear_reference(x, qw, sw, bias)
+
+
+@pytest.mark.parametrize("batch", [1, 17])
+def test_prepared_hybrid_output_split_on_two_streams_bit_exact(batch: int) -> None:
+    # Reference: test_prepared_w8a8_hybrid_output_split_matches_dynamic_reference_on_qpu (K=32, N=48, split 16).
+    x, weight, bias, expected = _plan_case(801 + batch, batch, 32, 48)
+    destination = torch.full((batch, 48), float("nan"), device="cuda")
+    with Queue() as first, Queue() as second, PreparedW8A8Linear(weight, max_batch=max(16, batch),
+                                                                 bias=dev(bias)) as plan:
+        event = plan.execute_hybrid(destination, dev(x), qpu_queue=first, cpu_queue=second, qpu_outputs=16)
+        event.wait()
+        assert event.name == "gfx950.w8a8_linear.hybrid_join"
+        np.testing.assert_array_equal(destination.cpu().numpy(), expected)
+        with pytest.raises(ValueError, match="aligned"):
+            plan.execute_hybrid(destination, dev(x), qpu_queue=first, cpu_queue=second, qpu_outputs=48)
+        with pytest.raises(DependencyError):
+            plan.execute_hybrid(destination, dev(x), qpu_queue=first, cpu_queue=first, qpu_outputs=16)
+
+
+def test_prepared_hybrid_row_split_pads_k_bit_exact() -> None:
+    # Reference: test_prepared_w8a8_hybrid_row_split_matches_dynamic_reference_on_qpu (31 x 20 -> 19, split 16).
+    x, weight, bias, expected = _plan_case(1907, 31, 20, 19)
+    destination = torch.full((31, 19), float("nan"), device="cuda")
+    with Queue() as first, Queue() as second, PreparedW8A8Linear(weight, max_batch=32, bias=dev(bias)) as plan:
+        plan.execute_hybrid_rows(destination, dev(x), qpu_queue=first, cpu_queue=second, qpu_rows=16).wait()
+        np.testing.assert_array_equal(destination.cpu().numpy(), expected)
+        # A strided source view goes through the plan's staging buffer.
+        wide = dev(np.concatenate([x, x], axis=1))[:, :20]
+        destination.fill_(float("nan"))
+        plan.execute_hybrid_rows(destination, wide, qpu_queue=first, cpu_queue=second, qpu_rows=16).wait()
+        np.testing.assert_array_equal(destination.cpu().numpy(), expected)
+
+
+def test_prepared_execute_prepared_reads_the_activation_workspace() -> None:
+    from qpu_xla_amd.kernels.quantize import quantize_rows_int8
+
+    x, weight, bias, expected = _plan_case(1731, 3, 64, 32)
+    destination = torch.empty((3, 32), device="cuda")
+    with Queue() as queue, PreparedW8A8Linear(weight, max_batch=4, bias=dev(bias)) as plan:
+        qa, sa = plan.activation_workspace
+        with torch.cuda.stream(queue.stream):
+            quantize_rows_int8(dev(x), out=qa, scales=sa, stream=queue)
+        plan.execute_prepared(destination, batch=3, queue=queue).wait()
+        np.testing.assert_array_equal(destination.cpu().numpy(), expected)
+
+
+def test_calibrated_auto_selects_the_fastest_exact_partition_axis() -> None:
+    # Reference: test_calibrated_w8a8_auto_selects_the_fastest_exact_partition_axis, with "gpu"
+    # records in place of the VideoCore "qpu" ones.
+    from qpu_xla_amd import Placement
+    from qpu_xla_amd.candidates import (CandidateRecord, CandidateRegistry, CandidateStatus, CorrectnessEvidence,
+                                        PartitionEvidence, PerformanceEvidence)
+    from qpu_xla_amd.quantization import CalibratedW8A8Linear
+
+    x, weight, _, _ = _plan_case(2921, 32, 16, 32)
+    qw, sw = weight.values.cpu().numpy(), weight.scales.cpu().numpy()
+    expected = oracle.w8a8_linear_reference(x, qw, sw, None)
+    exact = CorrectnessEvidence("oracle", 1, True, 0.0, 0.0, 0.0, 0.0)
+
+    def record(name, seconds, placement="gpu", partition=None):
+        return CandidateRecord(name, "linear", "w8a8-i32-fp32", "row-major-packed-k4", "32x16x32", "hash",
+                               CandidateStatus.SUPPORTED_WIN, exact, PerformanceEvidence("numpy", (0.010,), (seconds,)),
+                               placement=placement, partition=partition)
+
+    registry = CandidateRegistry((
+        record("gpu", 0.004),
+        record("hybrid-rows", 0.001, "hybrid", PartitionEvidence("rows", 16, 32, 16)),
+        record("hybrid-outputs", 0.002, "hybrid", PartitionEvidence("outputs", 16, 32, 16)),
+    ))
+    destination = torch.empty((32, 32), device="cuda")
+    with Queue() as first, Queue() as second, CalibratedW8A8Linear(weight, max_batch=32,
+                                                                   candidates=registry) as plan:
+        plan.execute(destination, dev(x), queue=first, cpu_queue=second).wait()
+        assert plan.last_dispatch.record.name == "hybrid-rows"
+        np.testing.assert_array_equal(destination.cpu().numpy(), expected)
+        destination.fill_(float("nan"))
+        plan.execute(destination, dev(x), queue=first, cpu_queue=second, qpu_outputs=16).wait()
+        assert plan.last_dispatch.record.name == "hybrid-outputs"
+        np.testing.assert_array_equal(destination.cpu().numpy(), expected)
+        destination.fill_(float("nan"))
+        event = plan.execute(destination, dev(x), queue=first)
+        event.wait()
+        assert plan.last_dispatch.record.name == "gpu" and event.name == "gfx950.w8a8_linear"
+        np.testing.assert_array_equal(destination.cpu().numpy(), expected)
+        with pytest.raises(ValueError, match="no CPU reference fallback"):
+            plan.execute(destination[:31], dev(x[:31]), queue=first)
+        with pytest.raises(ValueError, match="no CPU placement"):
+            plan.execute(destination, dev(x), queue=first, placement=Placement.CPU)
+    with CalibratedW8A8Linear(weight, max_batch=32, candidates=CandidateRegistry()) as empty:
+        assert empty._gpu is None
+        with pytest.raises(ValueError, match="no CPU reference fallback"):
+            empty.execute(destination, dev(x), queue=Queue())
