@@ -25,6 +25,12 @@ Pinning status (what each function is checked against, in ``tests/``):
   quantiser invariants including the 1/127 scale floor.
 * ``pack_q4_0_tiled_weights`` / ``split_q8_0_blocks``: byte-level checks of
   the word layout against the native blocks and exact inversion.
+* CPU_REPACK layouts (``unpack_q4_0x4`` / ``pack_q4_0x4``,
+  ``deinterleave_q8_0x4`` / ``interleave_q8_0x4``): exact inversion both
+  ways, the signed-nibble meaning of the 0x88 mask (each packed nibble is the
+  two's-complement 4-bit value code - 8), and the native-smoke expectation
+  that an interleaved activation gives the native result
+  (qpu_llama_q4_0_mx_smoke.c:47-180).
 * ``quantize_q4_0_blocks``: PARITY UNPINNED against upstream ggml
   ``quantize_row_q4_0`` (ggml is not vendored in the reference); only the
   BASELINE formula's invariants are checked.
@@ -34,7 +40,10 @@ from oracle.ggml import (  # noqa: F401
     Q4_0_BLOCK_BYTES,
     Q8_0_BLOCK_BYTES,
     QK,
+    deinterleave_q8_0x4,
+    interleave_q8_0x4,
     pack_q4_0_blocks,
+    pack_q4_0x4,
     pack_q4_0_tiled_weights,
     pack_q8_0_blocks,
     q4_0_q8_0_block_dots,
@@ -44,6 +53,7 @@ from oracle.ggml import (  # noqa: F401
     quantize_q8_0_split,
     split_q8_0_blocks,
     unpack_q4_0_blocks,
+    unpack_q4_0x4,
     unpack_q8_0_blocks,
 )
 from oracle.w8a8 import (  # noqa: F401

@@ -224,3 +224,101 @@ def split_q8_0_blocks(blocks: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     values = np.ascontiguousarray(blocks[..., 2:].reshape(rows, nblocks * QK))
     return scales, values
 
+
+
+# ------------------------------------------------ llama.cpp CPU_REPACK layouts
+
+REPACK_GROUP_BYTES = 4 * Q4_0_BLOCK_BYTES      # block_q4_0x4: 4 fp16 scales + 64 code bytes
+INTERLEAVED_BLOCK_BYTES = 4 * Q8_0_BLOCK_BYTES  # block_q8_0x4: 4 fp16 scales + 128 values
+
+
+def unpack_q4_0x4(groups: np.ndarray) -> np.ndarray:
+    """CPU_REPACK ``block_q4_0x4`` groups [N/4, B, 72] -> native Q4_0 blocks [N, B, 18].
+
+    Follows ``unpack_q4_0_4x4`` (``integrations/llama_cpp/backend/ggml-qpu.cpp:250-284``):
+    scale of column r at bytes 2r..2r+1; code bytes 4c..4c+3 of column r in
+    word 4c + r of the 64 code bytes, each byte XOR 0x88.
+    """
+    groups = np.asarray(groups, dtype=np.uint8)
+    if groups.ndim != 3 or groups.shape[2] != REPACK_GROUP_BYTES:
+        raise ValueError("CPU_REPACK groups must have shape [N/4, blocks, 72]")
+    n4, blocks, _ = groups.shape
+    out = np.empty((n4, 4, blocks, Q4_0_BLOCK_BYTES), dtype=np.uint8)
+    for row in range(4):
+        out[:, row, :, 0:2] = groups[:, :, 2 * row:2 * row + 2]
+        for chunk in range(4):
+            word = 8 + (chunk * 4 + row) * 4
+            out[:, row, :, 2 + 4 * chunk:6 + 4 * chunk] = groups[:, :, word:word + 4] ^ np.uint8(0x88)
+    return out.reshape(n4 * 4, blocks, Q4_0_BLOCK_BYTES)
+
+
+def pack_q4_0x4(blocks: np.ndarray) -> np.ndarray:
+    """Native Q4_0 blocks [N, B, 18] (N % 4 == 0) -> CPU_REPACK groups: the inverse of ``unpack_q4_0x4``."""
+    blocks = np.asarray(blocks, dtype=np.uint8)
+    if blocks.ndim != 3 or blocks.shape[2] != Q4_0_BLOCK_BYTES or blocks.shape[0] % 4:
+        raise ValueError("native Q4_0 blocks must have shape [N, blocks, 18] with N % 4 == 0")
+    n, nb, _ = blocks.shape
+    cols = blocks.reshape(n // 4, 4, nb, Q4_0_BLOCK_BYTES)
+    out = np.empty((n // 4, nb, REPACK_GROUP_BYTES), dtype=np.uint8)
+    for row in range(4):
+        out[:, :, 2 * row:2 * row + 2] = cols[:, row, :, 0:2]
+        for chunk in range(4):
+            word = 8 + (chunk * 4 + row) * 4
+            out[:, :, word:word + 4] = cols[:, row, :, 2 + 4 * chunk:6 + 4 * chunk] ^ np.uint8(0x88)
+    return out
+
+
+def _interleaved_index(index: int, lane: int, interleave: int) -> int:
+    # Position of value ``index`` of row ``lane`` inside a block_q8_0x4's 128 values
+    # (qpu_llama_q4_0.c:189-203).
+    return (index // interleave) * 4 * interleave + lane * interleave + index % interleave
+
+
+def interleave_q8_0x4(rows: np.ndarray, interleave: int) -> np.ndarray:
+    """Native Q8_0 rows [M, B, 34] -> CPU_REPACK activation bytes (same total size).
+
+    Follows the packer of ``integrations/llama_cpp/tests/qpu_llama_q4_0_mx_smoke.c:23-45``:
+    rows below M - M % 4 form block_q8_0x4 groups (the four scales, then the
+    values at ``_interleaved_index``); the remaining rows stay native.
+    """
+    rows = np.asarray(rows, dtype=np.uint8)
+    if interleave not in (4, 8) or rows.ndim != 3 or rows.shape[2] != Q8_0_BLOCK_BYTES:
+        raise ValueError("interleave must be 4 or 8 and rows [M, blocks, 34]")
+    m, nb, _ = rows.shape
+    out = rows.reshape(m, nb * Q8_0_BLOCK_BYTES).copy()
+    grouped = m - m % 4
+    perm = np.array([[_interleaved_index(i, lane, interleave) for i in range(QK)] for lane in range(4)])
+    for base in range(0, grouped, 4):
+        group = np.empty((nb, INTERLEAVED_BLOCK_BYTES), dtype=np.uint8)
+        for lane in range(4):
+            native = rows[base + lane]
+            group[:, 2 * lane:2 * lane + 2] = native[:, 0:2]
+            group[:, 8 + perm[lane]] = native[:, 2:]
+        out[base:base + 4] = group.reshape(4, nb * Q8_0_BLOCK_BYTES)
+    return out.reshape(-1)
+
+
+def deinterleave_q8_0x4(packed: np.ndarray, rows: int, blocks: int, interleave: int) -> np.ndarray:
+    """CPU_REPACK activation bytes -> native Q8_0 rows [M, B, 34].
+
+    Follows ``q8_0_source_block`` / ``q8_0_source_value``
+    (``integrations/llama_cpp/src/qpu_llama_q4_0.c:160-203``).
+    """
+    packed = np.asarray(packed, dtype=np.uint8).reshape(-1)
+    row_bytes = blocks * Q8_0_BLOCK_BYTES
+    if interleave not in (4, 8) or packed.size < rows * row_bytes:
+        raise ValueError("interleave must be 4 or 8 and the buffer must hold M rows")
+    out = np.empty((rows, blocks, Q8_0_BLOCK_BYTES), dtype=np.uint8)
+    grouped = rows - rows % 4
+    for row in range(rows):
+        for block in range(blocks):
+            if row < grouped:
+                group = (row // 4) * 4 * row_bytes + block * INTERLEAVED_BLOCK_BYTES
+                lane = row % 4
+                out[row, block, 0:2] = packed[group + 2 * lane:group + 2 * lane + 2]
+                for index in range(QK):
+                    out[row, block, 2 + index] = packed[group + 8 + _interleaved_index(index, lane, interleave)]
+            else:
+                start = row * row_bytes + block * Q8_0_BLOCK_BYTES
+                out[row, block] = packed[start:start + Q8_0_BLOCK_BYTES]
+    return out

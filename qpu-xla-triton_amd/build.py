@@ -8,6 +8,7 @@ Sources are compiled in parallel to objects under ``_build/`` and linked into
 from __future__ import annotations
 
 import concurrent.futures
+import hashlib
 import os
 import shutil
 import subprocess
@@ -48,9 +49,26 @@ def _hipcc() -> str:
     return found
 
 
-def _compile(source: Path) -> Path:
+def source_hash() -> str:
+    """SHA-256 over every kernel source and public header, in name order.
+
+    Compiled in as ``QXT_Q4_0_SOURCE_HASH`` and returned by
+    ``qxt_llama_q4_0_source_hash()``: the value a prepared linear's
+    ``expected_source_hash`` must carry.
+    """
+    digest = hashlib.sha256()
+    files = sorted([*CSRC.glob("*.hip"), *CSRC.glob("*.h"), *(REPO_ROOT / "include").glob("*.h")], key=lambda f: f.name)
+    for path in files:
+        digest.update(path.name.encode())
+        digest.update(b"\0")
+        digest.update(path.read_bytes())
+    return digest.hexdigest()
+
+
+def _compile(source: Path, defines: tuple[str, ...] = ()) -> Path:
     obj = BUILD_DIR / (source.stem + ".o")
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-I", str(REPO_ROOT / "include"), "-I", str(CSRC), "-c", str(source), "-o", str(obj)]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *defines, "-I", str(REPO_ROOT / "include"), "-I", str(CSRC), "-c", str(source),
+           "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed on {source.name}:\n{proc.stderr}")
@@ -68,8 +86,9 @@ def build(verbose: bool = True) -> Path:
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     workers = min(len(sources), int(os.environ.get("MAX_JOBS", "8")))
+    defines = (f'-DQXT_Q4_0_SOURCE_HASH="{source_hash()}"',)
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
-        objects = list(pool.map(_compile, sources))
+        objects = list(pool.map(lambda src: _compile(src, defines), sources))
     tmp = LIBRARY.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)

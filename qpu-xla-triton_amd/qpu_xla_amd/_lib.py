@@ -1,4 +1,5 @@
-"""ctypes binding of ``libqxt_gfx950.so`` (declared in ``include/qxt_gfx950.h``).
+"""ctypes binding of ``libqxt_gfx950.so`` (declared in ``include/qxt_gfx950.h``
+and ``include/qxt_llama_q4_0.h``).
 
 The library is built in-tree by ``qpu-xla-triton_amd/build.py``.  There is no
 fallback: when the library is missing every entry point raises
@@ -9,7 +10,19 @@ from __future__ import annotations
 
 import ctypes
 import threading
-from ctypes import POINTER, Structure, c_char, c_char_p, c_int, c_int32, c_int64, c_size_t, c_uint32, c_void_p
+from ctypes import (
+    POINTER,
+    Structure,
+    c_char,
+    c_char_p,
+    c_int,
+    c_int32,
+    c_int64,
+    c_size_t,
+    c_uint32,
+    c_uint64,
+    c_void_p,
+)
 from pathlib import Path
 from typing import Any
 
@@ -33,6 +46,7 @@ FAIL_DEVICE_OPEN = 1 << 0
 FAIL_ALLOCATION = 1 << 1
 FAIL_SUBMISSION = 1 << 2
 FAIL_WAIT = 1 << 3
+FAIL_SOURCE_HASH = 1 << 4  # llama bridge contexts only
 
 QUANT_NO_SCALE_FLOOR = 1
 WEIGHT_NK = 0
@@ -76,6 +90,56 @@ class Q4Task(Structure):
     ]
 
 
+class LlamaContextConfig(Structure):
+    """``qxt_llama_context_config``."""
+
+    _fields_ = [("device", c_int32), ("timeout_ns", c_uint64), ("failure_mask", c_uint32)]
+
+
+class LlamaQ4_0LinearDesc(Structure):
+    """``qxt_llama_q4_0_linear_desc`` (fields of qpu_llama_q4_0_linear_desc + weight_format)."""
+
+    _fields_ = [
+        ("weights", c_void_p),
+        ("weight_size", c_size_t),
+        ("input_columns", c_uint32),
+        ("output_columns", c_uint32),
+        ("rows", c_uint32),
+        ("resident_column_start", c_uint32),
+        ("resident_column_count", c_uint32),
+        ("weight_mode", c_int),
+        ("workgroups_per_supergroup", c_uint32),
+        ("expected_source_hash", c_char_p),
+        ("weight_format", c_int),
+    ]
+
+
+class LlamaQ4_0Execution(Structure):
+    """``qxt_llama_q4_0_execution`` (fields of qpu_llama_q4_0_execution)."""
+
+    _fields_ = [
+        ("activation", c_void_p),
+        ("activation_size", c_size_t),
+        ("activation_offset", c_size_t),
+        ("destination", c_void_p),
+        ("destination_size", c_size_t),
+        ("destination_offset", c_size_t),
+        ("column_start", c_uint32),
+        ("column_count", c_uint32),
+        ("rows", c_uint32),
+        ("activation_interleave", c_uint32),
+    ]
+
+
+class LlamaQ4_0Timing(Structure):
+    """``qxt_llama_q4_0_timing`` (fields of qpu_llama_q4_0_timing), nanoseconds."""
+
+    _fields_ = [(name, c_uint64) for name in (
+        "input_access_ns", "input_pack_ns", "input_sync_ns", "input_copy_ns", "submit_ns", "wait_ns",
+        "submit_wait_ns", "output_sync_ns", "output_copy_ns", "complete_ns",
+    )]
+
+
 _P = c_void_p
 _SZ = c_size_t
 _U = c_uint32
@@ -104,6 +168,18 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "qxt_w8a8_gemm_dequantize": (c_int, [_P, _SZ, _P, _SZ, _P, _P, _P, _P, _SZ, _U, _U, _U, _U, _P]),
     "qxt_w8a8_dequantize": (c_int, [_P, _SZ, _P, _P, _P, _P, _SZ, _U, _U, _P]),
     "qxt_w8a8_linear": (c_int, [_P, _SZ, _P, _SZ, _P, _P, _SZ, _P, _P, _P, _SZ, _U, _U, _U, _U, _U, _P]),
+    "qxt_llama_context_create": (c_int, [POINTER(LlamaContextConfig), POINTER(c_void_p)]),
+    "qxt_llama_context_destroy": (None, [_P]),
+    "qxt_llama_context_last_error": (c_char_p, [_P]),
+    "qxt_llama_context_set_failure_mask": (None, [_P, _U]),
+    "qxt_llama_q4_0_source_hash": (c_char_p, []),
+    "qxt_llama_q4_0_linear_prepare": (c_int, [_P, POINTER(LlamaQ4_0LinearDesc), POINTER(c_void_p)]),
+    "qxt_llama_q4_0_linear_destroy": (None, [_P]),
+    "qxt_llama_q4_0_linear_resident_bytes": (_SZ, [_P]),
+    "qxt_llama_q4_0_linear_submit": (c_int, [_P, POINTER(LlamaQ4_0Execution), POINTER(c_void_p)]),
+    "qxt_llama_q4_0_submission_wait": (c_int, [_P, POINTER(LlamaQ4_0Timing)]),
+    "qxt_llama_q4_0_submission_destroy": (None, [_P]),
+    "qxt_llama_q4_0_linear_execute": (c_int, [_P, POINTER(LlamaQ4_0Execution), POINTER(LlamaQ4_0Timing)]),
 }
 
 

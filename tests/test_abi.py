@@ -14,12 +14,15 @@ import pytest
 
 from qpu_xla_amd import _lib
 
-HEADER = Path(__file__).resolve().parents[1] / "include" / "qxt_gfx950.h"
+HEADERS = sorted((Path(__file__).resolve().parents[1] / "include").glob("*.h"))
 
 
 def declared_functions() -> list[str]:
-    text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(qxt_\w+)\s*\(", text, flags=re.MULTILINE)))
+    names: set[str] = set()
+    for header in HEADERS:
+        text = header.read_text()
+        names.update(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(qxt_\w+)\s*\(", text, flags=re.MULTILINE))
+    return sorted(names)
 
 
 def test_header_declares_the_boundary() -> None:
@@ -121,3 +124,38 @@ def test_q4_0_linear_rejects_k_beyond_the_lds_budget_before_launch() -> None:
     status = _lib.load().qxt_ggml_q4_0_q8_0_linear(FAKE, 4096 * 34, FAKE, 4096 * 18, FAKE, 64, 1, 4096, 0, 0, 16, None)
     assert status == _lib.CAPABILITY_MISSING
     assert "LDS" in _lib.last_error()
+
+
+def test_llama_bridge_source_hash_is_the_build_hash() -> None:
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("qxt_build", Path(__file__).resolve().parents[1] / "qpu-xla-triton_amd" / "build.py")
+    builder = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(builder)
+    from qpu_xla_amd import llama_bridge
+
+    value = llama_bridge.source_hash()
+    assert re.fullmatch(r"[0-9a-f]{64}", value)
+    assert value == builder.source_hash(), "library is stale: rebuild before testing"
+
+
+def test_llama_bridge_validates_on_the_host() -> None:
+    lib = _lib.load()
+    handle = ctypes.c_void_p()
+    assert lib.qxt_llama_context_create(None, None) == _lib.INVALID_ARGUMENT
+    injected = _lib.LlamaContextConfig(0, 0, _lib.FAIL_DEVICE_OPEN)
+    assert lib.qxt_llama_context_create(ctypes.byref(injected), ctypes.byref(handle)) == _lib.DEVICE_UNAVAILABLE
+    assert not handle.value
+    unknown = _lib.LlamaContextConfig(0, 0, 1 << 9)
+    assert lib.qxt_llama_context_create(ctypes.byref(unknown), ctypes.byref(handle)) == _lib.INVALID_ARGUMENT
+    desc = _lib.LlamaQ4_0LinearDesc()
+    assert lib.qxt_llama_q4_0_linear_prepare(None, ctypes.byref(desc), ctypes.byref(handle)) == _lib.INVALID_ARGUMENT
+    execution = _lib.LlamaQ4_0Execution()
+    assert lib.qxt_llama_q4_0_linear_submit(None, ctypes.byref(execution), ctypes.byref(handle)) == _lib.INVALID_ARGUMENT
+    assert lib.qxt_llama_q4_0_submission_wait(None, None) == _lib.INVALID_ARGUMENT
+    assert lib.qxt_llama_q4_0_linear_execute(None, None, None) == _lib.INVALID_ARGUMENT
+    assert lib.qxt_llama_q4_0_linear_resident_bytes(None) == 0
+    assert lib.qxt_llama_context_last_error(None) == b"no context"
+    lib.qxt_llama_q4_0_linear_destroy(None)
+    lib.qxt_llama_q4_0_submission_destroy(None)
+    lib.qxt_llama_context_destroy(None)

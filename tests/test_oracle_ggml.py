@@ -202,3 +202,67 @@ def test_split_q8_0_blocks_inverts_packing() -> None:
     assert q.shape == (4, 192)
     np.testing.assert_array_equal(scale_bits.view(np.float16), scales)
     np.testing.assert_array_equal(q.view(np.int8).reshape(4, 6, 32), values.astype(np.int8))
+
+
+# --------------------------------------------------------- CPU_REPACK layouts
+
+
+def test_repack_q4_0x4_inverts_exactly_both_ways() -> None:
+    rng = np.random.default_rng(44)
+    native = rng.integers(0, 256, size=(12, 3, oracle.Q4_0_BLOCK_BYTES), dtype=np.uint8)
+    groups = oracle.pack_q4_0x4(native)
+    assert groups.shape == (3, 3, 72)
+    np.testing.assert_array_equal(oracle.unpack_q4_0x4(groups), native)
+    raw = rng.integers(0, 256, size=(2, 5, 72), dtype=np.uint8)
+    np.testing.assert_array_equal(oracle.pack_q4_0x4(oracle.unpack_q4_0x4(raw)), raw)
+
+
+def test_repack_q4_0x4_nibbles_are_signed_values() -> None:
+    # ggml's repacked Q4_0 stores each element as a two's-complement nibble of
+    # (code - 8): that is what the 0x88 mask means.  Check every nibble of a
+    # packed group against the element it must carry.
+    rng = np.random.default_rng(45)
+    codes = rng.integers(0, 16, size=(4, 2, oracle.QK))
+    scales = rng.standard_normal((4, 2)).astype(np.float16)
+    groups = oracle.pack_q4_0x4(oracle.pack_q4_0_blocks(scales, codes))
+
+    def signed(nibble: np.ndarray) -> np.ndarray:
+        return np.where(nibble >= 8, nibble.astype(int) - 16, nibble.astype(int))
+
+    for column in range(4):
+        np.testing.assert_array_equal(groups[0, :, 2 * column:2 * column + 2].copy().view("<f2")[:, 0], scales[column])
+        for chunk in range(4):
+            word = groups[0, :, 8 + (chunk * 4 + column) * 4:8 + (chunk * 4 + column) * 4 + 4]
+            for byte in range(4):
+                element = 4 * chunk + byte
+                np.testing.assert_array_equal(signed(word[:, byte] & 0xF), codes[column, :, element] - 8)
+                np.testing.assert_array_equal(signed(word[:, byte] >> 4), codes[column, :, element + 16] - 8)
+
+
+@pytest.mark.parametrize("interleave", [4, 8])
+@pytest.mark.parametrize("rows", [1, 3, 4, 5, 8, 9])
+def test_q8_0x4_interleave_round_trip(rows: int, interleave: int) -> None:
+    rng = np.random.default_rng(rows * 10 + interleave)
+    native = rng.integers(0, 256, size=(rows, 2, oracle.Q8_0_BLOCK_BYTES), dtype=np.uint8)
+    packed = oracle.interleave_q8_0x4(native, interleave)
+    assert packed.size == native.size
+    np.testing.assert_array_equal(oracle.deinterleave_q8_0x4(packed, rows, 2, interleave), native)
+    tail = rows - rows % 4
+    row_bytes = 2 * oracle.Q8_0_BLOCK_BYTES
+    np.testing.assert_array_equal(packed[tail * row_bytes:], native[tail:].reshape(-1))
+    if rows >= 4:
+        # Each group is a permutation of its four native rows' bytes.
+        group = packed[:4 * row_bytes]
+        assert sorted(group.tolist()) == sorted(native[:4].reshape(-1).tolist())
+        assert not np.array_equal(group, native[:4].reshape(-1))
+
+
+@pytest.mark.parametrize("interleave", [4, 8])
+def test_q8_0x4_positions_cover_each_value_once(interleave: int) -> None:
+    from oracle.ggml import _interleaved_index
+
+    positions = sorted(_interleaved_index(i, lane, interleave) for lane in range(4) for i in range(oracle.QK))
+    assert positions == list(range(4 * oracle.QK))
+    # Runs of ``interleave`` consecutive values of one row stay contiguous.
+    assert all(_interleaved_index(i + 1, 2, interleave) == _interleaved_index(i, 2, interleave) + 1
+               for i in range(oracle.QK - 1) if (i + 1) % interleave)
