@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define QXT_ABI_VERSION 1
+#define QXT_ABI_VERSION 2
 
 /* Status values equal qpu_llama_status
  * (integrations/llama_cpp/include/qpu_llama_runtime.h:16-27). */
@@ -154,6 +154,36 @@ int qxt_ggml_q4_0_q8_0_linear(const void *activation, size_t activation_row_stri
                               uint32_t weight_column_start, uint32_t output_column_start,
                               uint32_t column_count, void *stream);
 
+/* Q4_0 weight layouts of the decode path (qxt_q4_0_task.weight_layout). */
+#define QXT_Q4_0_LAYOUT_NATIVE 0u /* ggml rows: [columns, blocks, 18] */
+#define QXT_Q4_0_LAYOUT_LANES 1u  /* qxt_q4_0_pack_lanes output */
+
+/* Bytes of the lane layout of a [columns, blocks, 18] Q4_0 matrix (0 when
+ * blocks % 8 != 0).  No reference counterpart. */
+size_t qxt_q4_0_lanes_bytes(uint32_t columns, uint32_t blocks);
+
+/* Repack native Q4_0 rows into the lane layout read by the decode kernels:
+ * the matrix is cut into units of 8 consecutive blocks of one column (144
+ * bytes, native order: unit u = column * blocks/8 + block/8), units into
+ * groups of 64, and chunk v (bytes 16v .. 16v+15) of unit l of group q is
+ * stored at q * 9216 + (v * 64 + l) * 16; units past the matrix are zero.
+ * Same bytes, no scale or code changes: the weight-preparation step of the
+ * reference's prepared linear (qpu_llama_q4_0.c:343-395, which also re-lays
+ * weights out for its kernel).  blocks % 8 == 0; weight and packed 16-byte
+ * aligned, weight_row_stride % 16 == 0; packed_bytes >= qxt_q4_0_lanes_bytes. */
+int qxt_q4_0_pack_lanes(const void *weight, size_t weight_row_stride, void *packed, size_t packed_bytes,
+                        uint32_t columns, uint32_t blocks, void *stream);
+
+/* qxt_ggml_q4_0_q8_0_linear over a lane-layout weight of `weight_columns`
+ * columns (weight_column_start + column_count <= weight_columns); same
+ * result bit for bit.  Any row count runs on v_dot4. */
+int qxt_ggml_q4_0_q8_0_linear_lanes(const void *activation, size_t activation_row_stride,
+                                    const void *packed_weight, uint32_t weight_columns,
+                                    float *destination, size_t destination_row_stride,
+                                    uint32_t rows, uint32_t blocks,
+                                    uint32_t weight_column_start, uint32_t output_column_start,
+                                    uint32_t column_count, void *stream);
+
 /* Prefill Q4_0 x Q8_0 linear over the reference's split / tiled operand layout:
  *   activation_q      int8 [rows, blocks*32] (the Q8_0 values, row stride in bytes, % 4 == 0),
  *   activation_scales fp16 bits [rows, blocks], elements of activation_scale_bytes = 2 (uint16)
@@ -190,7 +220,9 @@ int qxt_ggml_q4_0_q8_0_block_dots(const void *activation, size_t activation_row_
  * with 16-byte aligned rows, quantised to Q8_0 inside the kernel by the rule of
  * qxt_quantize_q8_0) and `activation` (native Q8_0 blocks) is non-NULL; the
  * other fields mean what they mean for qxt_ggml_q4_0_q8_0_linear.  Batched
- * tasks need rows <= 4, blocks % 8 == 0 and 16-byte aligned weight rows. */
+ * tasks need rows <= 4, blocks % 8 == 0 and 16-byte aligned weight rows.
+ * weight_layout QXT_Q4_0_LAYOUT_LANES: `weight` is the base of a
+ * qxt_q4_0_pack_lanes matrix and weight_row_stride is ignored. */
 typedef struct qxt_q4_0_task {
     const float *x;
     size_t x_row_stride;
@@ -205,6 +237,7 @@ typedef struct qxt_q4_0_task {
     uint32_t weight_column_start;
     uint32_t output_column_start;
     uint32_t column_count;
+    uint32_t weight_layout; /* QXT_Q4_0_LAYOUT_* */
 } qxt_q4_0_task;
 
 typedef struct qxt_q4_0_batch qxt_q4_0_batch;

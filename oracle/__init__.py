@@ -31,6 +31,9 @@ Pinning status (what each function is checked against, in ``tests/``):
   two's-complement 4-bit value code - 8), and the native-smoke expectation
   that an interleaved activation gives the native result
   (qpu_llama_q4_0_mx_smoke.c:47-180).
+* ``pack_q4_0_lanes``: exact inversion and the byte position of every
+  16-byte chunk (a layout of this library, checked against its definition
+  chunk by chunk; the kernels' parity is then pinned by the linear's oracle).
 * ``quantize_q4_0_blocks``: PARITY UNPINNED against upstream ggml
   ``quantize_row_q4_0`` (ggml is not vendored in the reference); only the
   BASELINE formula's invariants are checked.
@@ -43,6 +46,7 @@ from oracle.ggml import (  # noqa: F401
     deinterleave_q8_0x4,
     interleave_q8_0x4,
     pack_q4_0_blocks,
+    pack_q4_0_lanes,
     pack_q4_0x4,
     pack_q4_0_tiled_weights,
     pack_q8_0_blocks,
@@ -53,6 +57,7 @@ from oracle.ggml import (  # noqa: F401
     quantize_q8_0_split,
     split_q8_0_blocks,
     unpack_q4_0_blocks,
+    unpack_q4_0_lanes,
     unpack_q4_0x4,
     unpack_q8_0_blocks,
 )

@@ -322,3 +322,40 @@ def deinterleave_q8_0x4(packed: np.ndarray, rows: int, blocks: int, interleave: 
                 start = row * row_bytes + block * Q8_0_BLOCK_BYTES
                 out[row, block] = packed[start:start + Q8_0_BLOCK_BYTES]
     return out
+
+
+# ------------------------------------------------------ lane layout (decode)
+
+LANE_GROUP_UNITS = 64
+LANE_UNIT_BYTES = 8 * Q4_0_BLOCK_BYTES  # 144: 8 blocks of one column
+
+
+def pack_q4_0_lanes(blocks: np.ndarray) -> np.ndarray:
+    """Native Q4_0 blocks [N, B, 18] (B % 8 == 0) -> the lane layout (flat uint8).
+
+    The GPU library's decode-path weight layout (no reference counterpart; the
+    reference re-lays weights out for its own kernels at prepare time,
+    ``integrations/llama_cpp/src/qpu_llama_q4_0.c:343-395``): units of 144
+    bytes (8 blocks of one column, native order), groups of 64 units, chunk v
+    (16 bytes) of unit l of group q at ``q * 9216 + (v * 64 + l) * 16``; the
+    last group is zero-padded.
+    """
+    blocks = np.asarray(blocks, dtype=np.uint8)
+    if blocks.ndim != 3 or blocks.shape[2] != Q4_0_BLOCK_BYTES or blocks.shape[1] % 8:
+        raise ValueError("lane layout needs blocks [N, B, 18] with B % 8 == 0")
+    units = blocks.reshape(-1, LANE_UNIT_BYTES)
+    groups = -(-units.shape[0] // LANE_GROUP_UNITS)
+    padded = np.zeros((groups * LANE_GROUP_UNITS, LANE_UNIT_BYTES), dtype=np.uint8)
+    padded[: units.shape[0]] = units
+    chunks = padded.reshape(groups, LANE_GROUP_UNITS, 9, 16)
+    return np.ascontiguousarray(chunks.transpose(0, 2, 1, 3)).reshape(-1)
+
+
+def unpack_q4_0_lanes(packed: np.ndarray, columns: int, blocks: int) -> np.ndarray:
+    """Inverse of ``pack_q4_0_lanes``."""
+    packed = np.asarray(packed, dtype=np.uint8).reshape(-1)
+    units = columns * (blocks // 8)
+    groups = -(-units // LANE_GROUP_UNITS)
+    chunks = packed[: groups * LANE_GROUP_UNITS * LANE_UNIT_BYTES].reshape(groups, 9, LANE_GROUP_UNITS, 16)
+    unit_rows = chunks.transpose(0, 2, 1, 3).reshape(-1, LANE_UNIT_BYTES)[:units]
+    return np.ascontiguousarray(unit_rows).reshape(columns, blocks, Q4_0_BLOCK_BYTES)

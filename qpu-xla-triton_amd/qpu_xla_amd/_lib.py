@@ -49,6 +49,8 @@ FAIL_WAIT = 1 << 3
 FAIL_SOURCE_HASH = 1 << 4  # llama bridge contexts only
 
 QUANT_NO_SCALE_FLOOR = 1
+Q4_0_LAYOUT_NATIVE = 0
+Q4_0_LAYOUT_LANES = 1
 WEIGHT_NK = 0
 WEIGHT_K4N = 1
 
@@ -87,6 +89,7 @@ class Q4Task(Structure):
         ("weight_column_start", c_uint32),
         ("output_column_start", c_uint32),
         ("column_count", c_uint32),
+        ("weight_layout", c_uint32),
     ]
 
 
@@ -159,6 +162,9 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "qxt_quantize_q4_0": (c_int, [_P, _SZ, _P, _SZ, _U, _U, _P]),
     "qxt_ggml_q4_0_q8_0_linear": (c_int, [_P, _SZ, _P, _SZ, _P, _SZ, _U, _U, _U, _U, _U, _P]),
     "qxt_ggml_q4_0_q8_0_block_dots": (c_int, [_P, _SZ, _P, _SZ, _P, _U, _U, _U, _U, _P]),
+    "qxt_q4_0_lanes_bytes": (_SZ, [_U, _U]),
+    "qxt_q4_0_pack_lanes": (c_int, [_P, _SZ, _P, _SZ, _U, _U, _P]),
+    "qxt_ggml_q4_0_q8_0_linear_lanes": (c_int, [_P, _SZ, _P, _U, _P, _SZ, _U, _U, _U, _U, _U, _P]),
     "qxt_ggml_q4_0_q8_0_tiled_linear": (c_int, [_P, _SZ, _P, _SZ, _U, _P, _SZ, _P, _SZ, _P, _SZ, _U, _U, _U, _P]),
     "qxt_q4_0_batch_prepare": (c_int, [POINTER(Q4Task), _U, POINTER(c_void_p)]),
     "qxt_q4_0_batch_launch": (c_int, [_P, _P]),

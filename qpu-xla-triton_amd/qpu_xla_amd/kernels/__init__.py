@@ -14,11 +14,14 @@ from qpu_xla_amd.kernels.gemv_int8 import W8A8_GEMV_KERNEL, supports_w8a8_gemv  
 from qpu_xla_amd.kernels.ggml_q4_0 import (  # noqa: F401
     GGML_Q4_0_Q8_0_LINEAR_KERNEL,
     GGML_Q4_0_Q8_0_TILED_LINEAR_KERNEL,
+    Q4_0LaneWeights,
     Q4_0LinearBatch,
     ggml_q4_0_q8_0_block_dots,
+    ggml_q4_0_q8_0_lane_linear,
     ggml_q4_0_q8_0_linear,
     ggml_q4_0_q8_0_tiled_linear,
     pack_ggml_q4_0_blocks,
+    pack_ggml_q4_0_lane_weights,
     pack_ggml_q4_0_tiled_weights,
     pack_ggml_q8_0_blocks,
     split_ggml_q8_0_blocks,

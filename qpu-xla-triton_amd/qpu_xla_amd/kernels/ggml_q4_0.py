@@ -182,6 +182,94 @@ def ggml_q4_0_q8_0_linear(
     return destination
 
 
+# ------------------------------------------------------------- lane layout
+# Decode-path weight layout (qxt_q4_0_pack_lanes): the native rows' 144-byte
+# units (8 blocks of one column) in groups of 64, chunk v of unit l of a group
+# at (v * 64 + l) * 16, so every 16-byte load instruction of a wave reads one
+# contiguous kilobyte.  Same bytes, prepared once like the reference's
+# prepared-linear weight upload (qpu_llama_q4_0.c:343-395).
+
+LANE_GROUP_UNITS = 64
+LANE_UNIT_BYTES = 144
+
+
+class Q4_0LaneWeights:
+    """A Q4_0 matrix [columns, blocks, 18] held in the lane layout (uint8 device tensor)."""
+
+    def __init__(self, packed: torch.Tensor, columns: int, blocks: int) -> None:
+        need = lanes_bytes(columns, blocks)
+        if packed.dtype != torch.uint8 or packed.dim() != 1 or packed.numel() < need or not packed.is_contiguous():
+            raise ValueError("lane weights must be a contiguous uint8 tensor of qxt_q4_0_lanes_bytes bytes")
+        self.packed = packed
+        self.columns = int(columns)
+        self.blocks = int(blocks)
+
+    @property
+    def device(self) -> torch.device:
+        return self.packed.device
+
+    @property
+    def shape(self) -> tuple[int, int, int]:
+        """Shape of the native matrix this holds."""
+        return (self.columns, self.blocks, Q4_0_BLOCK_BYTES)
+
+
+def lanes_bytes(columns: int, blocks: int) -> int:
+    """Bytes of the lane layout (whole 64-unit groups); needs blocks % 8 == 0."""
+    if columns <= 0 or blocks <= 0 or blocks % 8:
+        raise ValueError("the lane layout needs columns > 0 and blocks % 8 == 0")
+    units = columns * (blocks // 8)
+    return -(-units // LANE_GROUP_UNITS) * LANE_GROUP_UNITS * LANE_UNIT_BYTES
+
+
+def pack_ggml_q4_0_lane_weights(weight: torch.Tensor, *, stream: Any = None) -> Q4_0LaneWeights:
+    """Repack native Q4_0 blocks uint8 [N, B, 18] (B % 8 == 0) into the lane layout on the GPU."""
+    if weight.dtype != torch.uint8 or weight.dim() != 3 or weight.shape[2] != Q4_0_BLOCK_BYTES or not weight.is_contiguous():
+        raise ValueError("pack_ggml_q4_0_lane_weights: contiguous uint8 [N, B, 18] blocks are required")
+    columns, blocks, _ = weight.shape
+    packed = torch.empty(lanes_bytes(columns, blocks), dtype=torch.uint8, device=weight.device)
+    require_gpu("pack_ggml_q4_0_lane_weights", weight, packed)
+    _lib.call("qxt_q4_0_pack_lanes", ptr(weight), row_stride(weight), ptr(packed), packed.numel(), columns, blocks,
+              stream_handle(stream))
+    return Q4_0LaneWeights(packed, columns, blocks)
+
+
+def ggml_q4_0_q8_0_lane_linear(
+    activation: torch.Tensor,
+    weight: Q4_0LaneWeights,
+    destination: torch.Tensor | None = None,
+    *,
+    weight_column_start: int = 0,
+    output_column_start: int = 0,
+    column_count: int | None = None,
+    stream: Any = None,
+) -> torch.Tensor:
+    """``ggml_q4_0_q8_0_linear`` over lane-layout weights (same result bit for bit)."""
+    if activation.dim() != 3 or activation.dtype != torch.uint8 or activation.shape[2] != Q8_0_BLOCK_BYTES:
+        raise ValueError("ggml_q4_0_q8_0_lane_linear: activation must be uint8 [M, B, 34]")
+    rows, blocks = activation.shape[0], activation.shape[1]
+    if blocks != weight.blocks or not activation.is_contiguous():
+        raise ValueError("ggml_q4_0_q8_0_lane_linear: contiguous activation with the weight's block count required")
+    if column_count is None:
+        column_count = weight.columns - weight_column_start
+    if destination is None:
+        destination = torch.empty((rows, output_column_start + column_count), dtype=torch.float32, device=weight.device)
+    if destination.dtype != torch.float32 or not rows_are_dense(destination):
+        raise ValueError("ggml_q4_0_q8_0_lane_linear: float32 destination with contiguous rows required")
+    if weight_column_start < 0 or weight_column_start + column_count > weight.columns:
+        raise ValueError("ggml_q4_0_q8_0_lane_linear: weight column range out of bounds")
+    if output_column_start < 0 or output_column_start + column_count > destination.shape[1] or destination.shape[0] != rows:
+        raise ValueError("ggml_q4_0_q8_0_lane_linear: destination too small")
+    require_gpu("ggml_q4_0_q8_0_lane_linear", activation, weight.packed, destination)
+    _lib.call(
+        "qxt_ggml_q4_0_q8_0_linear_lanes",
+        ptr(activation), row_stride(activation), ptr(weight.packed), weight.columns,
+        ptr(destination), row_stride(destination),
+        rows, blocks, weight_column_start, output_column_start, column_count, stream_handle(stream),
+    )
+    return destination
+
+
 def ggml_q4_0_q8_0_block_dots(
     activation: torch.Tensor,
     weight: torch.Tensor,
@@ -330,7 +418,8 @@ def ggml_q4_0_q8_0_tiled_linear(
 class Q4_0LinearBatch:
     """Independent Q4_0 x Q8_0 linears computed by one kernel launch.
 
-    Each task is a dict with ``weight`` (uint8 [N, B, 18]), ``destination``
+    Each task is a dict with ``weight`` (uint8 [N, B, 18], or a
+    ``Q4_0LaneWeights`` from ``pack_ggml_q4_0_lane_weights``), ``destination``
     (float32 [rows, >= N]) and exactly one of ``x`` (float32 [rows, B*32]:
     quantised to Q8_0 inside the kernel, same rule as ``quantize_q8_0``) or
     ``activation`` (native Q8_0 uint8 [rows, B, 34]); optional
@@ -356,10 +445,17 @@ class Q4_0LinearBatch:
             activation = spec.get("activation")
             if (x is None) == (activation is None):
                 raise ValueError("each task needs exactly one of 'x' and 'activation'")
-            if weight.dtype != torch.uint8 or weight.dim() != 3 or weight.shape[2] != Q4_0_BLOCK_BYTES:
-                raise ValueError("task weight must be uint8 [N, B, 18]")
-            if not weight.is_contiguous() or destination.dtype != torch.float32 or not rows_are_dense(destination):
-                raise ValueError("task weight must be contiguous and destination float32 with contiguous rows")
+            lanes = isinstance(weight, Q4_0LaneWeights)
+            if lanes:
+                weight_tensor = weight.packed
+            else:
+                weight_tensor = weight
+                if weight.dtype != torch.uint8 or weight.dim() != 3 or weight.shape[2] != Q4_0_BLOCK_BYTES:
+                    raise ValueError("task weight must be uint8 [N, B, 18] or Q4_0LaneWeights")
+                if not weight.is_contiguous():
+                    raise ValueError("task weight must be contiguous")
+            if destination.dtype != torch.float32 or not rows_are_dense(destination):
+                raise ValueError("task destination must be float32 with contiguous rows")
             blocks = weight.shape[1]
             source = x if x is not None else activation
             rows = source.shape[0]
@@ -380,9 +476,10 @@ class Q4_0LinearBatch:
                     raise ValueError("task activation must be contiguous uint8 [rows, B, 34]")
                 table[i].activation = activation.data_ptr()
                 table[i].activation_row_stride = row_stride(activation)
-            require_gpu("Q4_0LinearBatch", source, weight, destination)
-            table[i].weight = weight.data_ptr()
-            table[i].weight_row_stride = row_stride(weight)
+            require_gpu("Q4_0LinearBatch", source, weight_tensor, destination)
+            table[i].weight = weight_tensor.data_ptr()
+            table[i].weight_row_stride = 0 if lanes else row_stride(weight_tensor)
+            table[i].weight_layout = _lib.Q4_0_LAYOUT_LANES if lanes else _lib.Q4_0_LAYOUT_NATIVE
             table[i].destination = destination.data_ptr()
             table[i].destination_row_stride = row_stride(destination)
             table[i].rows = rows
@@ -390,7 +487,7 @@ class Q4_0LinearBatch:
             table[i].weight_column_start = wcol0
             table[i].output_column_start = ocol0
             table[i].column_count = ncols
-            self._tensors.extend(t for t in (x, activation, weight, destination) if t is not None)
+            self._tensors.extend(t for t in (x, activation, weight_tensor, destination) if t is not None)
         handle = ctypes.c_void_p()
         _lib.check(_lib.load().qxt_q4_0_batch_prepare(table, len(tasks), ctypes.byref(handle)))
         self._handle = handle

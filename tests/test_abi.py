@@ -49,7 +49,7 @@ def test_binding_covers_exactly_the_header() -> None:
 
 def test_status_strings_and_version() -> None:
     lib = _lib.load()
-    assert lib.qxt_abi_version() == 1
+    assert lib.qxt_abi_version() == 2
     assert _lib.status_string(_lib.OK) == "ok"
     assert _lib.status_string(_lib.SUBMISSION_FAILED) == "submission failed"
     assert _lib.status_string(_lib.TIMEOUT) == "timeout"

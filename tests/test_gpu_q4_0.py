@@ -329,3 +329,72 @@ def test_native_linear_prefill_rows_run_on_matrix_cores_bit_exact(rows: int, blo
     out = destination.cpu().numpy()
     np.testing.assert_array_equal(out[:, :16], SENTINEL)
     np.testing.assert_array_equal(out[:, 16:], oracle.q4_0_q8_0_reference(act, wt[wcol0:wcol0 + ncols]))
+
+
+# ------------------------------------------------------------- lane layout
+
+
+@pytest.mark.parametrize("n,blocks", [(5632, 64), (37, 176), (2048, 176), (3, 8)])
+def test_lane_pack_kernel_matches_the_layout_definition(n: int, blocks: int) -> None:
+    rng = np.random.default_rng(n + blocks)
+    native = rng.integers(0, 256, size=(n, blocks, 18), dtype=np.uint8)
+    lanes = q4.pack_ggml_q4_0_lane_weights(dev(native))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(lanes.packed.cpu().numpy(), oracle.pack_q4_0_lanes(native))
+    assert lanes.packed.numel() == _lib.load().qxt_q4_0_lanes_bytes(n, blocks)
+
+
+@pytest.mark.parametrize("rows,k,n,wcol0,ncols", [
+    (1, 2048, 5632, 0, 5632),   # cfg0
+    (4, 4096, 4096, 0, 4096),   # cfg2 (K=4096, N=4096)
+    (1, 5632, 2048, 16, 2032),  # a column range starting inside a lane group
+    (2, 256, 37, 5, 31),        # a partial last group, any column range
+    (17, 512, 64, 0, 64),       # rows beyond one MFMA-free row group
+])
+def test_lane_linear_bit_exact_against_oracle(rows: int, k: int, n: int, wcol0: int, ncols: int) -> None:
+    rng = np.random.default_rng(5000 + rows + n)
+    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    x = rng.standard_normal((rows, k), dtype=np.float32)
+    wq, xq = oracle.quantize_q4_0_blocks(w), oracle.quantize_q8_0_blocks(x)
+    lanes = q4.pack_ggml_q4_0_lane_weights(dev(wq))
+    out = torch.full((rows, ncols + 16), float(SENTINEL), device="cuda")
+    q4.ggml_q4_0_q8_0_lane_linear(dev(xq), lanes, out, weight_column_start=wcol0, output_column_start=16,
+                                  column_count=ncols)
+    got = out.cpu().numpy()
+    np.testing.assert_array_equal(got[:, :16], SENTINEL)
+    np.testing.assert_array_equal(got[:, 16:], oracle.q4_0_q8_0_reference(xq, wq[wcol0:wcol0 + ncols]))
+
+
+def test_lane_batch_matches_native_batch_and_oracle() -> None:
+    shapes = [(1, 2048, 2048, 0, 2048), (1, 2048, 256, 0, 256), (1, 5632, 2048, 0, 2048),
+              (1, 2048, 5632, 0, 5632), (1, 256, 48, 16, 17), (4, 4096, 100, 3, 90)]
+    tasks, expected = _batch_case(36, shapes)
+    lane_tasks = []
+    for t in tasks:
+        lt = dict(t)
+        lt["weight"] = q4.pack_ggml_q4_0_lane_weights(t["weight"])
+        lt["destination"] = torch.full_like(t["destination"], float(SENTINEL))
+        lane_tasks.append(lt)
+    with q4.Q4_0LinearBatch(tasks) as native, q4.Q4_0LinearBatch(lane_tasks) as lanes:
+        assert lanes.work_items == native.work_items
+        native.launch()
+        lanes.launch()
+        torch.cuda.synchronize()
+    _check_batch(tasks, expected)
+    _check_batch(lane_tasks, expected)
+
+
+def test_lane_entry_points_validate_before_launching() -> None:
+    lib = _lib.load()
+    assert lib.qxt_q4_0_lanes_bytes(10, 12) == 0 and lib.qxt_q4_0_lanes_bytes(0, 8) == 0
+    assert lib.qxt_q4_0_lanes_bytes(65, 8) == 2 * 9216
+    w = torch.zeros((8, 8, 18), dtype=torch.uint8, device="cuda")
+    small = torch.zeros(9216 - 16, dtype=torch.uint8, device="cuda")
+    status = lib.qxt_q4_0_pack_lanes(w.data_ptr(), 144, small.data_ptr(), small.numel(), 8, 8, None)
+    assert status == _lib.INVALID_ARGUMENT
+    lanes = q4.pack_ggml_q4_0_lane_weights(w)
+    act = torch.zeros((1, 8, 34), dtype=torch.uint8, device="cuda")
+    out = torch.zeros((1, 16), device="cuda")
+    status = lib.qxt_ggml_q4_0_q8_0_linear_lanes(act.data_ptr(), 272, lanes.packed.data_ptr(), 8, out.data_ptr(), 64,
+                                                  1, 8, 4, 0, 8, None)
+    assert status == _lib.INVALID_ARGUMENT and "past the packed matrix" in _lib.last_error()

@@ -266,3 +266,23 @@ def test_q8_0x4_positions_cover_each_value_once(interleave: int) -> None:
     # Runs of ``interleave`` consecutive values of one row stay contiguous.
     assert all(_interleaved_index(i + 1, 2, interleave) == _interleaved_index(i, 2, interleave) + 1
                for i in range(oracle.QK - 1) if (i + 1) % interleave)
+
+
+@pytest.mark.parametrize("n,blocks", [(1, 8), (5, 16), (64, 8), (37, 176), (130, 24)])
+def test_lane_layout_places_every_chunk_and_inverts(n: int, blocks: int) -> None:
+    rng = np.random.default_rng(n * blocks)
+    native = rng.integers(0, 256, size=(n, blocks, oracle.Q4_0_BLOCK_BYTES), dtype=np.uint8)
+    packed = oracle.pack_q4_0_lanes(native)
+    units = native.reshape(-1, 144)
+    groups = -(-units.shape[0] // 64)
+    assert packed.size == groups * 64 * 144
+    for unit in range(units.shape[0]):
+        q, lane = divmod(unit, 64)
+        for v in range(9):
+            at = q * 9216 + (v * 64 + lane) * 16
+            np.testing.assert_array_equal(packed[at:at + 16], units[unit, 16 * v:16 * v + 16])
+    tail = units.shape[0] % 64
+    if tail:  # padding units of the last group are zero
+        last = packed[(groups - 1) * 9216:].reshape(9, 64, 16)
+        assert not last[:, tail:].any()
+    np.testing.assert_array_equal(oracle.unpack_q4_0_lanes(packed, n, blocks), native)
