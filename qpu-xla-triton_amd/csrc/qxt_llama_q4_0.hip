@@ -5,7 +5,8 @@
 //   prepare  -- validate, check the source hash, allocate every buffer once
 //               (device weights/activation/output, pinned host staging),
 //               upload the resident columns (CPU_REPACK groups are unpacked
-//               by a kernel), then never allocate again;
+//               by a kernel; decode-sized linears keep them in the lane
+//               layout), then never allocate again;
 //   submit   -- host rows -> pinned staging -> HBM on the context's stream,
 //               CPU_REPACK Q8_0x4 rows de-interleaved by a kernel, the Q4_0
 //               linear over the selected columns, the selected output columns
@@ -170,7 +171,9 @@ struct qxt_llama_q4_0_linear {
     size_t activation_row_bytes = 0;  // blocks * 34
     size_t output_row_bytes = 0;      // resident_count * 4
     size_t resident_bytes = 0;
-    void *weight = nullptr;           // device Q4_0 [resident_count][blocks]
+    size_t weight_bytes = 0;
+    bool lanes = false;               // weight in the lane layout (decode-sized linears)
+    void *weight = nullptr;           // device Q4_0 [resident_count][blocks] (native or lane layout)
     void *activation = nullptr;       // device Q8_0 [rows][blocks]
     void *activation_packed = nullptr;  // device copy of interleaved host rows
     float *output = nullptr;          // device fp32 [rows][resident_count]
@@ -223,33 +226,45 @@ void end_submission(qxt_llama_q4_0_linear *l, bool poison) {
     l->busy = false;
 }
 
-// Copy the resident weight columns to the device, unpacking CPU_REPACK groups.
+// Copy the resident weight columns to the device, unpacking CPU_REPACK groups
+// and, for decode-sized linears, re-laying the native rows out in the lane
+// layout the decode kernels stream fastest (qxt_q4_0_pack_lanes).
 int upload_weights(qxt_llama_q4_0_linear *l, const qxt_llama_q4_0_linear_desc *d) {
     qxt_llama_context *ctx = l->context;
     const size_t bytes = static_cast<size_t>(l->resident_count) * l->weight_row_bytes;
-    // Columns [start, start + count) occupy the same byte range in both layouts
-    // (a CPU_REPACK group of 4 columns is 4 native rows long, start % 4 == 0).
+    // Columns [start, start + count) occupy the same byte range in both host
+    // layouts (a CPU_REPACK group of 4 columns is 4 native rows long, start % 4 == 0).
     const uint8_t *src = static_cast<const uint8_t *>(d->weights) + l->resident_start * l->weight_row_bytes;
+    const bool repack = d->weight_format == QXT_LLAMA_Q4_0_FORMAT_REPACK_4X4;
+    void *raw = nullptr;     // host bytes as uploaded, when they are not yet native rows
+    void *native = nullptr;  // native rows, when they are not the final layout
     hipError_t err = hipSuccess;
-    if (d->weight_format == QXT_LLAMA_Q4_0_FORMAT_NATIVE) {
-        err = hipMemcpyAsync(l->weight, src, bytes, hipMemcpyHostToDevice, ctx->stream);
-    } else {
-        void *staged = nullptr;
-        err = hipMalloc(&staged, bytes);
-        if (err != hipSuccess) return ctx->fail(QXT_ALLOCATION_FAILED, "weight staging: %s", hipGetErrorString(err));
-        err = hipMemcpyAsync(staged, src, bytes, hipMemcpyHostToDevice, ctx->stream);
-        if (err == hipSuccess) {
-            const size_t items = static_cast<size_t>(l->resident_count) * l->blocks;
-            hipLaunchKernelGGL(unpack_q4_0x4_kernel, dim3(grid_for(items, 256)), dim3(256), 0, ctx->stream,
-                               static_cast<const uint8_t *>(staged), static_cast<uint8_t *>(l->weight),
-                               l->resident_count, l->blocks);
-            err = hipGetLastError();
-        }
-        hipError_t sync = hipStreamSynchronize(ctx->stream);
-        (void)hipFree(staged);
-        if (err == hipSuccess) err = sync;
+    if (repack) err = hipMalloc(&raw, bytes);
+    if (err == hipSuccess && l->lanes) err = hipMalloc(&native, bytes);
+    if (err != hipSuccess) {
+        (void)hipFree(raw);
+        return ctx->fail(QXT_ALLOCATION_FAILED, "weight staging: %s", hipGetErrorString(err));
     }
-    if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
+    void *rows = l->lanes ? native : l->weight;
+    err = hipMemcpyAsync(repack ? raw : rows, src, bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (err == hipSuccess && repack) {
+        const size_t items = static_cast<size_t>(l->resident_count) * l->blocks;
+        hipLaunchKernelGGL(unpack_q4_0x4_kernel, dim3(grid_for(items, 256)), dim3(256), 0, ctx->stream,
+                           static_cast<const uint8_t *>(raw), static_cast<uint8_t *>(rows), l->resident_count,
+                           l->blocks);
+        err = hipGetLastError();
+    }
+    int rc = QXT_OK;
+    if (err == hipSuccess && l->lanes) {
+        rc = qxt_q4_0_pack_lanes(native, l->weight_row_bytes, l->weight, l->weight_bytes, l->resident_count, l->blocks,
+                                 ctx->stream);
+        if (rc != QXT_OK) rc = ctx->fail(rc, "weight re-layout: %s", qxt_last_error());
+    }
+    const hipError_t sync = hipStreamSynchronize(ctx->stream);
+    (void)hipFree(raw);
+    (void)hipFree(native);
+    if (err == hipSuccess) err = sync;
+    if (rc != QXT_OK) return rc;
     if (err != hipSuccess) return ctx->fail(QXT_IO_FAILED, "weight upload: %s", hipGetErrorString(err));
     return QXT_OK;
 }
@@ -360,10 +375,17 @@ extern "C" int qxt_llama_q4_0_linear_prepare(qxt_llama_context *context, const q
     l->weight_row_bytes = weight_row_bytes;
     l->activation_row_bytes = act_row;
     l->output_row_bytes = out_row;
-    l->resident_bytes = resident_weight + 2 * act_bytes + out_bytes + act_bytes + out_bytes;
+    // Linears of fewer than 16 rows run on the v_dot4 decode kernel, which
+    // streams the lane layout fastest; prefill-sized ones on the matrix cores
+    // over native rows.
+    l->lanes = d->rows < 16 && blocks % 8 == 0;
+    l->weight_bytes = l->lanes ? qxt_q4_0_lanes_bytes(d->resident_column_count, static_cast<uint32_t>(blocks))
+                               : resident_weight;
+    // Device: weight, activation (+ its interleaved landing copy), output; pinned: activation, output.
+    l->resident_bytes = l->weight_bytes + 2 * act_bytes + out_bytes + act_bytes + out_bytes;
 
     DeviceScope scope(context->device);
-    hipError_t err = hipMalloc(&l->weight, resident_weight);
+    hipError_t err = hipMalloc(&l->weight, l->weight_bytes);
     if (err == hipSuccess) err = hipMalloc(&l->activation, act_bytes);
     if (err == hipSuccess) err = hipMalloc(&l->activation_packed, act_bytes);
     if (err == hipSuccess) err = hipMalloc(reinterpret_cast<void **>(&l->output), out_bytes);
@@ -466,9 +488,12 @@ extern "C" int qxt_llama_q4_0_linear_submit(qxt_llama_q4_0_linear *l, const qxt_
     s->submit_start = s->input_copy_end;
     int rc = QXT_OK;
     if (err == hipSuccess) {
-        rc = qxt_ggml_q4_0_q8_0_linear(l->activation, l->activation_row_bytes, l->weight, l->weight_row_bytes,
-                                       l->output, l->output_row_bytes, rows, l->blocks, local, local,
-                                       e->column_count, ctx->stream);
+        rc = l->lanes ? qxt_ggml_q4_0_q8_0_linear_lanes(l->activation, l->activation_row_bytes, l->weight,
+                                                        l->resident_count, l->output, l->output_row_bytes, rows,
+                                                        l->blocks, local, local, e->column_count, ctx->stream)
+                      : qxt_ggml_q4_0_q8_0_linear(l->activation, l->activation_row_bytes, l->weight,
+                                                  l->weight_row_bytes, l->output, l->output_row_bytes, rows, l->blocks,
+                                                  local, local, e->column_count, ctx->stream);
         if (rc != QXT_OK) rc = ctx->fail(QXT_SUBMISSION_FAILED, "q4_0 linear: %s", qxt_last_error());
     }
     if (rc == QXT_OK && err == hipSuccess) {
