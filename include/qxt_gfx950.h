@@ -216,6 +216,21 @@ int qxt_ggml_q4_0_q8_0_block_dots(const void *activation, size_t activation_row_
                                   uint32_t weight_column_start, uint32_t column_count,
                                   void *stream);
 
+/* ------------------------------------------------------- Q8_0 x Q8_0 linear */
+
+/* destination[r, output_column_start + j] =
+ *   sum_b fl32(fl32(float(dot_b) * da[r, b]) * dw[wc, b]) in block order (activation scale
+ * first, as ggml_q8_0_q8_0_reference, src/qpu_xla/kernels/ggml_q8_0.py:26-51),
+ * wc = weight_column_start + j.  activation and weight: native Q8_0 u8 [*, blocks, 34].
+ * Any rows (the reference kernel takes exactly 4) and any column range.  Replaces
+ * GGML_Q8_0_Q8_0_LINEAR_M4_KERNEL (ggml_q8_0.py:233-291). */
+int qxt_ggml_q8_0_q8_0_linear(const void *activation, size_t activation_row_stride,
+                              const void *weight, size_t weight_row_stride,
+                              float *destination, size_t destination_row_stride,
+                              uint32_t rows, uint32_t blocks,
+                              uint32_t weight_column_start, uint32_t output_column_start,
+                              uint32_t column_count, void *stream);
+
 /* One linear of a Q4_0 batch.  Exactly one of `x` (fp32 rows [rows, blocks*32]
  * with 16-byte aligned rows, quantised to Q8_0 inside the kernel by the rule of
  * qxt_quantize_q8_0) and `activation` (native Q8_0 blocks) is non-NULL; the

@@ -31,6 +31,10 @@ Pinning status (what each function is checked against, in ``tests/``):
   two's-complement 4-bit value code - 8), and the native-smoke expectation
   that an interleaved activation gives the native result
   (qpu_llama_q4_0_mx_smoke.c:47-180).
+* ``q8_0_q8_0_reference``: the reference's own check against the explicit
+  dequantised float dot (tests/test_qpu_xla_ggml_q8_0.py:16-31), a Python
+  brute force of the int32 block dots with power-of-two scales (exact), and
+  a case where scaling by dw first would round differently.
 * ``pack_q4_0_lanes``: exact inversion and the byte position of every
   16-byte chunk (a layout of this library, checked against its definition
   chunk by chunk; the kernels' parity is then pinned by the linear's oracle).
@@ -52,6 +56,7 @@ from oracle.ggml import (  # noqa: F401
     pack_q8_0_blocks,
     q4_0_q8_0_block_dots,
     q4_0_q8_0_reference,
+    q8_0_q8_0_reference,
     quantize_q4_0_blocks,
     quantize_q8_0_blocks,
     quantize_q8_0_split,

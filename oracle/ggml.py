@@ -359,3 +359,35 @@ def unpack_q4_0_lanes(packed: np.ndarray, columns: int, blocks: int) -> np.ndarr
     chunks = packed[: groups * LANE_GROUP_UNITS * LANE_UNIT_BYTES].reshape(groups, 9, LANE_GROUP_UNITS, 16)
     unit_rows = chunks.transpose(0, 2, 1, 3).reshape(-1, LANE_UNIT_BYTES)[:units]
     return np.ascontiguousarray(unit_rows).reshape(columns, blocks, Q4_0_BLOCK_BYTES)
+
+
+# ------------------------------------------------------------ Q8_0 x Q8_0
+
+
+def q8_0_q8_0_reference(activation_blocks: np.ndarray, weight_blocks: np.ndarray) -> np.ndarray:
+    """Q8_0 x Q8_0 linear: exact int32 block dots, scaled by da then dw, summed in block order.
+
+    Follows ``ggml_q8_0_q8_0_reference`` (``src/qpu_xla/kernels/ggml_q8_0.py:26-51``):
+    ``contribution = float32(dots); contribution *= da; contribution *= dw;
+    result += contribution`` per block, all in float32.
+    """
+    activation_blocks = np.asarray(activation_blocks, dtype=np.uint8)
+    weight_blocks = np.asarray(weight_blocks, dtype=np.uint8)
+    if activation_blocks.ndim != 3 or weight_blocks.ndim != 3:
+        raise ValueError("activation and weight blocks must both be rank three")
+    rows, blocks, a_bytes = activation_blocks.shape
+    outputs, w_blocks, w_bytes = weight_blocks.shape
+    if a_bytes != Q8_0_BLOCK_BYTES or w_bytes != Q8_0_BLOCK_BYTES or blocks != w_blocks:
+        raise ValueError("native Q8_0 block extents or counts do not match")
+    da, qa = unpack_q8_0_blocks(activation_blocks)
+    dw, qw = unpack_q8_0_blocks(weight_blocks)
+    da = da.astype(np.float32)
+    dw = dw.astype(np.float32)
+    result = np.zeros((rows, outputs), dtype=np.float32)
+    for b in range(blocks):
+        dots = qa[:, b].astype(np.int32) @ qw[:, b].astype(np.int32).T
+        term = dots.astype(np.float32)
+        term *= da[:, b, None]
+        term *= dw[None, :, b]
+        result += term
+    return result

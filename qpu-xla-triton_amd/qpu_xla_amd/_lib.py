@@ -162,6 +162,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "qxt_quantize_q4_0": (c_int, [_P, _SZ, _P, _SZ, _U, _U, _P]),
     "qxt_ggml_q4_0_q8_0_linear": (c_int, [_P, _SZ, _P, _SZ, _P, _SZ, _U, _U, _U, _U, _U, _P]),
     "qxt_ggml_q4_0_q8_0_block_dots": (c_int, [_P, _SZ, _P, _SZ, _P, _U, _U, _U, _U, _P]),
+    "qxt_ggml_q8_0_q8_0_linear": (c_int, [_P, _SZ, _P, _SZ, _P, _SZ, _U, _U, _U, _U, _U, _P]),
     "qxt_q4_0_lanes_bytes": (_SZ, [_U, _U]),
     "qxt_q4_0_pack_lanes": (c_int, [_P, _SZ, _P, _SZ, _U, _U, _P]),
     "qxt_ggml_q4_0_q8_0_linear_lanes": (c_int, [_P, _SZ, _P, _U, _P, _SZ, _U, _U, _U, _U, _U, _P]),

@@ -30,5 +30,10 @@ from qpu_xla_amd.kernels.ggml_q4_0 import (  # noqa: F401
     unpack_ggml_q4_0_blocks,
     unpack_ggml_q8_0_blocks,
 )
+from qpu_xla_amd.kernels.ggml_q8_0 import (  # noqa: F401
+    GGML_Q8_0_Q8_0_LINEAR_M4_KERNEL,
+    ggml_q8_0_q8_0_linear,
+    supports_ggml_q8_0_q8_0_linear_m4,
+)
 from qpu_xla_amd.kernels.quantize import quantize_q4_0, quantize_q8_0, quantize_rows_int8  # noqa: F401
 from qpu_xla_amd.kernels.w8a8_epilogue import W8A8_DEQUANTIZE_KERNEL, supports_w8a8_dequantize, w8a8_dequantize  # noqa: F401

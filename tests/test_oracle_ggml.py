@@ -286,3 +286,55 @@ def test_lane_layout_places_every_chunk_and_inverts(n: int, blocks: int) -> None
         last = packed[(groups - 1) * 9216:].reshape(9, 64, 16)
         assert not last[:, tail:].any()
     np.testing.assert_array_equal(oracle.unpack_q4_0_lanes(packed, n, blocks), native)
+
+
+# ------------------------------------------------------------ Q8_0 x Q8_0
+
+
+def _q8_operands(seed: int, rows: int, outputs: int, blocks: int, a_range=(-0.1, 0.1), w_range=(-0.2, 0.2)):
+    rng = np.random.default_rng(seed)
+    a_scales = rng.uniform(*a_range, size=(rows, blocks)).astype(np.float16)
+    a_values = rng.integers(-128, 128, size=(rows, blocks, 32), dtype=np.int16)
+    w_scales = rng.uniform(*w_range, size=(outputs, blocks)).astype(np.float16)
+    w_values = rng.integers(-128, 128, size=(outputs, blocks, 32), dtype=np.int16)
+    return (oracle.pack_q8_0_blocks(a_scales, a_values), oracle.pack_q8_0_blocks(w_scales, w_values),
+            a_scales, a_values, w_scales, w_values)
+
+
+def test_q8_0_reference_matches_the_explicit_dequantized_dot() -> None:
+    # tests/test_qpu_xla_ggml_q8_0.py:16-31 of the reference (seed 4850, same tolerance).
+    act, wt, a_s, a_v, w_s, w_v = _q8_operands(4850, 4, 3, 3)
+    actual = oracle.q8_0_q8_0_reference(act, wt)
+    activation = a_s.astype(np.float32)[..., None] * a_v.astype(np.float32)
+    weights = w_s.astype(np.float32)[..., None] * w_v.astype(np.float32)
+    expected = np.einsum("rbk,obk->ro", activation, weights, dtype=np.float32)
+    np.testing.assert_allclose(actual, expected, rtol=2e-5, atol=2e-3)
+
+
+def test_q8_0_reference_exact_with_power_of_two_scales() -> None:
+    rng = np.random.default_rng(4851)
+    rows, outputs, blocks = 3, 5, 4
+    a_s = (2.0 ** rng.integers(-6, 2, size=(rows, blocks))).astype(np.float16)
+    w_s = (2.0 ** rng.integers(-6, 2, size=(outputs, blocks))).astype(np.float16)
+    a_v = rng.integers(-128, 128, size=(rows, blocks, 32))
+    w_v = rng.integers(-128, 128, size=(outputs, blocks, 32))
+    got = oracle.q8_0_q8_0_reference(oracle.pack_q8_0_blocks(a_s, a_v), oracle.pack_q8_0_blocks(w_s, w_v))
+    for r in range(rows):
+        for o in range(outputs):
+            exact = sum(int(np.dot(a_v[r, b], w_v[o, b])) * float(a_s[r, b]) * float(w_s[o, b]) for b in range(blocks))
+            assert got[r, o] == np.float32(exact)  # every partial sum is exact in fp32 here
+
+
+def test_q8_0_reference_scales_by_the_activation_first() -> None:
+    # Find operands where fl(fl(dot*da)*dw) != fl(fl(dot*dw)*da): the oracle must give the first.
+    for seed in range(200):
+        act, wt, *_ = _q8_operands(seed, 1, 1, 1, a_range=(-1.0, 1.0), w_range=(-1.0, 1.0))
+        da, qa = oracle.unpack_q8_0_blocks(act)
+        dw, qw = oracle.unpack_q8_0_blocks(wt)
+        dot = float(np.dot(qa[0, 0].astype(np.int64), qw[0, 0].astype(np.int64)))
+        a_first = np.float32(np.float32(dot * float(da[0, 0])) * float(dw[0, 0]))
+        w_first = np.float32(np.float32(dot * float(dw[0, 0])) * float(da[0, 0]))
+        if a_first != w_first:
+            assert oracle.q8_0_q8_0_reference(act, wt)[0, 0] == a_first
+            return
+    pytest.fail("no order-sensitive case found")
