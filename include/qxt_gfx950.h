@@ -232,8 +232,8 @@ int qxt_ggml_q8_0_q8_0_linear(const void *activation, size_t activation_row_stri
                               uint32_t column_count, void *stream);
 
 /* One linear of a Q4_0 batch.  Exactly one of `x` (fp32 rows [rows, blocks*32]
- * with 16-byte aligned rows, quantised to Q8_0 inside the kernel by the rule of
- * qxt_quantize_q8_0) and `activation` (native Q8_0 blocks) is non-NULL; the
+ * with 16-byte aligned rows, quantised to Q8_0 by the rule of qxt_quantize_q8_0
+ * in a pre-pass launch of the batch) and `activation` (native Q8_0 blocks) is non-NULL; the
  * other fields mean what they mean for qxt_ggml_q4_0_q8_0_linear.  Batched
  * tasks need rows <= 4, blocks % 8 == 0 and 16-byte aligned weight rows.
  * weight_layout QXT_Q4_0_LAYOUT_LANES: `weight` is the base of a
@@ -259,12 +259,14 @@ typedef struct qxt_q4_0_batch qxt_q4_0_batch;
 
 /* Prepare a batch of independent Q4_0 x Q8_0 linears that one kernel launch
  * computes (e.g. every projection of a decode step); uploads a small task
- * table with hipMalloc/hipMemcpy (synchronous).  The tensors the tasks point
+ * table and allocates the Q8_0 buffer of the tasks' fp32 activations with
+ * hipMalloc/hipMemcpy (synchronous).  The tensors the tasks point
  * at must outlive the batch.  Replaces the prepared-linear handle
  * qpu_llama_q4_0_linear_prepare (integrations/llama_cpp/include/qpu_llama_q4_0.h:63-66). */
 int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_batch **batch);
 
-/* Enqueue the whole batch on `stream` (one launch; graph-capturable).
+/* Enqueue the whole batch on `stream`: the Q8_0 pre-pass (when a task has fp32
+ * rows) and the batch grid, two launches; graph-capturable.
  * Replaces qpu_llama_q4_0_linear_submit (qpu_llama_q4_0.h:72-75). */
 int qxt_q4_0_batch_launch(const qxt_q4_0_batch *batch, void *stream);
 

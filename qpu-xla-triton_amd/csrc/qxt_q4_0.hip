@@ -14,9 +14,7 @@
 //   phase 0  each thread issues the loads of its U units into registers;
 //   phase 1  while those loads are in flight the workgroup stages the Q8_0
 //            activation rows in LDS (int8 words + fp32 scale + int32 element
-//            sum per block), either from native 34-byte blocks or by
-//            quantising fp32 activations itself (the Q8_0 rule of
-//            quantize_q8_0_split, examples/benchmark_llama_cpp_qpu_persistent_q4.py:42-53);
+//            sum per block) from native 34-byte blocks;
 //   phase 2  each unit yields 8 block terms c_b (v_dot4_i32_i8) into LDS;
 //   phase 3  one thread per (row, column) adds the column's c_b in block
 //            order and stores the fp32 result.
@@ -40,7 +38,13 @@
 // Entry points: a single linear (stateless, native Q8_0 activation), its
 // int32 block-dot debug twin, and a prepared batch of independent linears
 // launched as one grid (the decode step of a model whose projections read
-// separate activations).
+// separate activations).  A batch task may give fp32 activation rows: one
+// pre-pass launch quantises all of them to Q8_0 (the rule of
+// quantize_q8_0_split, examples/benchmark_llama_cpp_qpu_persistent_q4.py:42-53)
+// into a buffer the batch owns, before the batch grid reads them as native
+// blocks.  (Quantising inside every workgroup instead -- each workgroup of a
+// linear re-quantising the whole row -- measured 86-97 us per cfg3 step
+// against 79-81 us with the pre-pass.)
 #include <algorithm>
 #include <new>
 #include <type_traits>
@@ -55,12 +59,11 @@ constexpr int kThreads = 256;
 constexpr size_t kMaxLds = 64 * 1024;
 
 struct Q4Task {
-    const float *x;        // fp32 activation rows, quantised in-kernel (batch only); else nullptr
-    const uint8_t *act;    // native Q8_0 blocks [rows, blocks, 34] when x == nullptr
+    const uint8_t *act;    // native Q8_0 blocks [rows, blocks, 34]
     const uint8_t *w;      // Q4_0 blocks [N, blocks, 18]
     float *y;              // fp32 output
     int32_t *dots;         // debug: int32 block dots [rows, ncols, blocks]
-    size_t x_stride, act_stride, w_stride, y_stride;  // row strides in bytes
+    size_t act_stride, w_stride, y_stride;  // row strides in bytes
     int rows, blocks, wcol0, ocol0, ncols, cpw;
     int lanes;             // weight in the lane-interleaved layout (w = packed matrix base)
 };
@@ -135,47 +138,6 @@ __device__ __forceinline__ int block_dot(const uint32_t (&qs)[4], const int *aq,
 template <int MR>
 __device__ __forceinline__ void stage_activation(const Q4Task &t, int r0, int *aq, int *ad, const Q4Lds &geo) {
     const int B = t.blocks;
-    if (t.x != nullptr) {
-        // Quantise fp32 rows to Q8_0 in place: 8 lanes per block, float4 per lane.
-        // Same arithmetic as q8_0_kernel: d = absmax / 127, inv = 1 / d (0 when
-        // d == 0), q = clamp(rint(x * inv), +-127); the dot uses the fp16-rounded d.
-        for (int e = threadIdx.x; e < MR * B * 8; e += kThreads) {
-            const int r = e / (B * 8);
-            const int rem = e - r * B * 8;
-            const int b = rem >> 3;
-            const int l8 = rem & 7;
-            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (r0 + r < t.rows)
-                v = *reinterpret_cast<const float4 *>(reinterpret_cast<const uint8_t *>(t.x) + (r0 + r) * t.x_stride +
-                                                      (b * QK + l8 * 4) * 4);
-            float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-            amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
-            amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
-            amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
-            const float d = amax / 127.0f;
-            const float inv = (d != 0.0f) ? 1.0f / d : 0.0f;
-            int q[4];
-            const float xs[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int c = static_cast<int>(rintf(xs[i] * inv));
-                q[i] = c < -127 ? -127 : (c > 127 ? 127 : c);
-            }
-            int sum = q[0] + q[1] + q[2] + q[3];
-            sum += __shfl_xor(sum, 1, 8);
-            sum += __shfl_xor(sum, 2, 8);
-            sum += __shfl_xor(sum, 4, 8);
-            const uint32_t word = (static_cast<uint32_t>(q[0]) & 0xFFu) | ((static_cast<uint32_t>(q[1]) & 0xFFu) << 8) |
-                                  ((static_cast<uint32_t>(q[2]) & 0xFFu) << 16) |
-                                  ((static_cast<uint32_t>(q[3]) & 0xFFu) << 24);
-            aq[r * geo.aq_row + aq_index(b, l8)] = static_cast<int>(word);
-            if (l8 == 0) {
-                ad[r * geo.ad_row + ad_index(b)] = __float_as_int(half_bits_to_float(float_to_half_bits(d)));
-                ad[r * geo.ad_row + ad_index(b) + 1] = sum;
-            }
-        }
-        return;
-    }
     for (int idx = threadIdx.x; idx < MR * B; idx += kThreads) {
         const int r = idx / B;
         const int b = idx - r * B;
@@ -255,6 +217,55 @@ __global__ __launch_bounds__(kThreads) void pack_lanes_kernel(const uint8_t *__r
         x = *reinterpret_cast<const v4u *>(w + col * w_stride + g * kUnitBytes + v * 16);
     }
     *reinterpret_cast<v4u *>(packed + idx * 16) = x;
+}
+
+// One fp32 activation of a batch to quantise: rows x blocks Q8_0 blocks.
+struct Q8Job {
+    const float *x;
+    size_t x_stride;
+    uint8_t *out;     // Q8_0 [rows, blocks, 34], row stride blocks * 34
+    int rows, blocks;
+};
+
+// Workgroup c quantises blocks [first, first + 32) of job `job` (8 lanes per
+// block, one float4 each), the arithmetic of q8_0_kernel: d = absmax / 127,
+// inv = 1 / d (0 for a zero block), q = clamp(rint(x * inv), +-127), d stored
+// as fp16 (round to nearest even).
+struct Q8Chunk {
+    int job;
+    int first;
+};
+
+__global__ __launch_bounds__(kThreads) void q8_0_prepass_kernel(const Q8Job *__restrict__ jobs,
+                                                                const Q8Chunk *__restrict__ chunks) {
+    const Q8Chunk c = chunks[blockIdx.x];
+    const Q8Job j = jobs[c.job];
+    const int gb = c.first + static_cast<int>(threadIdx.x >> 3);
+    const int l8 = threadIdx.x & 7;
+    if (gb >= j.rows * j.blocks) return;  // whole 8-lane groups exit together
+    const int row = gb / j.blocks;
+    const int b = gb - row * j.blocks;
+    const float *src = reinterpret_cast<const float *>(reinterpret_cast<const uint8_t *>(j.x) + row * j.x_stride) +
+                       b * QK + l8 * 4;
+    const v4u raw = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(src));
+    const float xs[4] = {__uint_as_float(raw[0]), __uint_as_float(raw[1]), __uint_as_float(raw[2]),
+                         __uint_as_float(raw[3])};
+    float amax = fmaxf(fmaxf(fabsf(xs[0]), fabsf(xs[1])), fmaxf(fabsf(xs[2]), fabsf(xs[3])));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
+    const float d = amax / 127.0f;
+    const float inv = (d != 0.0f) ? 1.0f / d : 0.0f;
+    int q[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = clamp127(rintf(xs[i] * inv));
+    uint8_t *dst = j.out + (static_cast<size_t>(row) * j.blocks + b) * Q8_0_BYTES;
+    const uint32_t word = pack_bytes(q[0], q[1], q[2], q[3]);
+    // Block bytes 2 + 4 * l8 .. are 2-byte aligned: two half-word stores.
+    uint16_t *h = reinterpret_cast<uint16_t *>(dst + 2 + 4 * l8);
+    h[0] = static_cast<uint16_t>(word & 0xFFFFu);
+    h[1] = static_cast<uint16_t>(word >> 16);
+    if (l8 == 0) *reinterpret_cast<uint16_t *>(dst) = static_cast<uint16_t>(float_to_half_bits(d));
 }
 
 // Phase 2 of the fast path for one round of U units per thread (units
@@ -507,11 +518,15 @@ int validate_q4(const void *activation, size_t activation_row_stride, const void
 using namespace qxt;
 
 struct qxt_q4_0_batch {
-    void *device_tables = nullptr;  // [Q4Task x count][Q4Item x items]
+    void *device_tables = nullptr;  // [Q4Task x count][Q4Item x items][Q8Job x jobs][Q8Chunk x chunks]
+    void *q8_staging = nullptr;     // Q8_0 blocks of the fp32 activations the pre-pass quantises
     const Q4Task *tasks = nullptr;
     const Q4Item *items = nullptr;
+    const Q8Job *jobs = nullptr;
+    const Q8Chunk *chunks = nullptr;
     uint32_t task_count = 0;
     uint32_t item_count = 0;
+    uint32_t chunk_count = 0;
     uint32_t grid = 0;
     int mr = 1;
     size_t lds = 0;
@@ -653,6 +668,8 @@ int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_
     *out = nullptr;
     if (tasks == nullptr || count == 0) return fail(QXT_INVALID_ARGUMENT, "q4_0 batch: no tasks");
     std::vector<Q4Task> host(count);
+    std::vector<Q8Job> jobs;
+    std::vector<uint32_t> job_task;
     uint32_t max_rows = 1;
     for (uint32_t i = 0; i < count; ++i) {
         const qxt_q4_0_task &d = tasks[i];
@@ -681,10 +698,16 @@ int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_
             static_cast<uint64_t>(d.output_column_start) + d.column_count > (1ull << 31))
             return fail(QXT_INVALID_ARGUMENT, "q4_0 batch task %u: column range overflows", i);
         Q4Task t{};
-        t.x = d.x;
-        t.x_stride = d.x_row_stride;
-        t.act = static_cast<const uint8_t *>(d.activation);
-        t.act_stride = d.activation_row_stride;
+        if (d.x != nullptr) {
+            // Quantised by the pre-pass into the batch's staging buffer (pointer patched below).
+            jobs.push_back({d.x, d.x_row_stride, nullptr, static_cast<int>(d.rows), static_cast<int>(d.blocks)});
+            job_task.push_back(i);
+            t.act = nullptr;
+            t.act_stride = static_cast<size_t>(d.blocks) * Q8_0_BYTES;
+        } else {
+            t.act = static_cast<const uint8_t *>(d.activation);
+            t.act_stride = d.activation_row_stride;
+        }
         t.w = static_cast<const uint8_t *>(d.weight);
         t.lanes = d.weight_layout == QXT_Q4_0_LAYOUT_LANES;
         t.w_stride = t.lanes ? static_cast<size_t>(d.blocks) * Q4_0_BYTES : d.weight_row_stride;
@@ -713,28 +736,58 @@ int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_
             items.push_back({static_cast<int>(i), c, std::min(host[i].cpw, host[i].ncols - c)});
     }
     if (items.size() > 0x7FFFFFFFu) return fail(QXT_INVALID_ARGUMENT, "q4_0 batch: too many work items");
+    std::vector<Q8Chunk> chunks;
+    size_t staging_bytes = 0;
+    std::vector<size_t> job_offset(jobs.size());
+    for (size_t j = 0; j < jobs.size(); ++j) {
+        job_offset[j] = staging_bytes;
+        const int nblocks = jobs[j].rows * jobs[j].blocks;
+        staging_bytes += (static_cast<size_t>(nblocks) * Q8_0_BYTES + 255) & ~size_t(255);
+        for (int first = 0; first < nblocks; first += kThreads / 8) chunks.push_back({static_cast<int>(j), first});
+    }
+    if (chunks.size() > 0x7FFFFFFFu) return fail(QXT_INVALID_ARGUMENT, "q4_0 batch: too many activation blocks");
     int rc = injected(QXT_FAIL_ALLOCATION);
     if (rc != QXT_OK) return rc;
     auto *batch = new (std::nothrow) qxt_q4_0_batch();
     if (batch == nullptr) return fail(QXT_ALLOCATION_FAILED, "q4_0 batch: host allocation failed");
-    const size_t task_bytes = (sizeof(Q4Task) * count + 255) & ~size_t(255);
-    const size_t bytes = task_bytes + sizeof(Q4Item) * items.size();
-    if (hipMalloc(&batch->device_tables, bytes) != hipSuccess) {
+    auto round = [](size_t b) { return (b + 255) & ~size_t(255); };
+    const size_t task_bytes = round(sizeof(Q4Task) * count);
+    const size_t item_bytes = round(sizeof(Q4Item) * items.size());
+    const size_t job_bytes = round(sizeof(Q8Job) * jobs.size());
+    const size_t bytes = task_bytes + item_bytes + job_bytes + sizeof(Q8Chunk) * chunks.size();
+    if (hipMalloc(&batch->device_tables, bytes) != hipSuccess ||
+        (staging_bytes > 0 && hipMalloc(&batch->q8_staging, staging_bytes) != hipSuccess)) {
+        if (batch->device_tables != nullptr) (void)hipFree(batch->device_tables);
         delete batch;
-        return fail(QXT_ALLOCATION_FAILED, "q4_0 batch: hipMalloc of %zu bytes failed", bytes);
+        return fail(QXT_ALLOCATION_FAILED, "q4_0 batch: hipMalloc of %zu + %zu bytes failed", bytes, staging_bytes);
+    }
+    for (size_t j = 0; j < jobs.size(); ++j) {
+        uint8_t *dst = static_cast<uint8_t *>(batch->q8_staging) + job_offset[j];
+        jobs[j].out = dst;
+        host[job_task[j]].act = dst;
     }
     auto *base = static_cast<uint8_t *>(batch->device_tables);
-    if (hipMemcpy(base, host.data(), sizeof(Q4Task) * count, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(base + task_bytes, items.data(), sizeof(Q4Item) * items.size(), hipMemcpyHostToDevice) !=
-            hipSuccess) {
+    bool ok = hipMemcpy(base, host.data(), sizeof(Q4Task) * count, hipMemcpyHostToDevice) == hipSuccess &&
+              hipMemcpy(base + task_bytes, items.data(), sizeof(Q4Item) * items.size(), hipMemcpyHostToDevice) ==
+                  hipSuccess;
+    if (ok && !jobs.empty())
+        ok = hipMemcpy(base + task_bytes + item_bytes, jobs.data(), sizeof(Q8Job) * jobs.size(),
+                       hipMemcpyHostToDevice) == hipSuccess &&
+             hipMemcpy(base + task_bytes + item_bytes + job_bytes, chunks.data(), sizeof(Q8Chunk) * chunks.size(),
+                       hipMemcpyHostToDevice) == hipSuccess;
+    if (!ok) {
         (void)hipFree(batch->device_tables);
+        if (batch->q8_staging != nullptr) (void)hipFree(batch->q8_staging);
         delete batch;
         return fail(QXT_IO_FAILED, "q4_0 batch: upload of the task tables failed");
     }
     batch->tasks = reinterpret_cast<const Q4Task *>(base);
     batch->items = reinterpret_cast<const Q4Item *>(base + task_bytes);
+    batch->jobs = reinterpret_cast<const Q8Job *>(base + task_bytes + item_bytes);
+    batch->chunks = reinterpret_cast<const Q8Chunk *>(base + task_bytes + item_bytes + job_bytes);
     batch->task_count = count;
     batch->item_count = static_cast<uint32_t>(items.size());
+    batch->chunk_count = static_cast<uint32_t>(chunks.size());
     batch->grid = static_cast<uint32_t>(items.size());
     batch->mr = mr;
     batch->lds = lds;
@@ -746,6 +799,11 @@ int qxt_q4_0_batch_launch(const qxt_q4_0_batch *batch, void *stream) {
     if (batch == nullptr) return fail(QXT_INVALID_ARGUMENT, "q4_0 batch: null handle");
     int rc = injected(QXT_FAIL_SUBMISSION);
     if (rc != QXT_OK) return rc;
+    if (batch->chunk_count > 0) {
+        rc = launch("q8_0_prepass_kernel", q8_0_prepass_kernel, dim3(batch->chunk_count), dim3(kThreads), 0,
+                    as_stream(stream), batch->jobs, batch->chunks);
+        if (rc != QXT_OK) return rc;
+    }
     return launch("q4_0_batch_kernel", batch_kernel(batch->mr), dim3(batch->grid), dim3(kThreads), batch->lds,
                   as_stream(stream), batch->tasks, batch->items);
 }
@@ -755,6 +813,7 @@ uint32_t qxt_q4_0_batch_work_items(const qxt_q4_0_batch *batch) { return batch =
 void qxt_q4_0_batch_destroy(qxt_q4_0_batch *batch) {
     if (batch == nullptr) return;
     if (batch->device_tables != nullptr) (void)hipFree(batch->device_tables);
+    if (batch->q8_staging != nullptr) (void)hipFree(batch->q8_staging);
     delete batch;
 }
 
