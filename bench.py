@@ -17,7 +17,7 @@ Also reported on the same JSON line:
   * ``configs``       -- cfg0 (rotated over >= 512 MB of weight copies), cfg1, cfg2;
   * ``cpu_baseline``  -- the NumPy oracle of the reference CPU path on this host.
 
-Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--legs decode,w8a8,cfg0,cfg1,cfg2,copy,cpu]
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--legs decode,w8a8,gemv,prefill,geglu,cfg0,cfg1,cfg2,copy,cpu]
 Weights and activations are synthetic (seeded random, the BASELINE distributions).
 """
 
@@ -68,7 +68,7 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--legs", default="decode,w8a8,gemv,prefill,cfg0,cfg1,cfg2,copy,cpu")
+    ap.add_argument("--legs", default="decode,w8a8,gemv,prefill,geglu,cfg0,cfg1,cfg2,copy,cpu")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of each CPU-baseline sample")
     return ap.parse_args()
 
@@ -570,6 +570,51 @@ def leg_prefill(torch, args) -> dict:
     return out
 
 
+def leg_geglu(torch, args) -> dict:
+    """GEGLU -> Q8_0 producer at the FFN width 5632: M = 1 (decode), 512 and 2048 (prefill).
+
+    HBM-bound: per 32-element block it reads 256 B of fp32 gate + up and
+    writes one 34-byte Q8_0 block (290 algorithmic bytes); the 128 KB GELU
+    table is read through the caches.  Launches rotate over enough buffer
+    sets (> 320 MB) that every launch reads its inputs from HBM, not from the
+    256 MB last-level cache.
+    """
+    from qpu_xla_amd.kernels.ggml_geglu_q8 import ggml_gelu_fp16_table
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(7)
+    table = ggml_gelu_fp16_table("cuda")
+    k = 5632
+    out = {}
+    for rows in (1, 512, 2048):
+        nsets = min(64, max(2, -(-(320 << 20) // (rows * k * 8))))
+        sets = [
+            (torch.randn((rows, k), generator=gen, device="cuda"), torch.randn((rows, k), generator=gen, device="cuda"),
+             torch.empty((rows, k // 32, 34), dtype=torch.uint8, device="cuda"))
+            for _ in range(nsets)
+        ]
+        runner = Runner(torch, torch.cuda.Stream())
+        for gate, up, q8 in sets:
+            runner.add("qxt_ggml_geglu_q8_0", _p(gate), _rs(gate), _p(up), _rs(up), _p(table), _p(q8), _rs(q8),
+                       rows, k, runner.handle)
+        runner.run()
+        torch.cuda.synchronize()
+        times = runner.kernel_times(repeats=max(1, 64 // nsets))
+        us = float(np.mean(next(v for name, v in times.items() if name.startswith("geglu_q8_0")))) * 1e3
+        nbytes = rows * (k // 32) * (256 + 34)
+        out[f"m{rows}"] = {
+            "shape": f"M={rows} K={k}",
+            "buffer_sets": nsets,
+            "kernel_us": us,
+            "bytes_per_launch": nbytes,
+            "gbs": nbytes / (us * 1e-6) / 1e9,
+            "frac_hbm_peak": nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS,
+        }
+        del sets
+        torch.cuda.empty_cache()
+    return out
+
+
 def leg_cfg1(torch, args) -> dict:
     """cfg1: W8A8 M=K=N=512 whole operator (launch-bound; parity case, reported only)."""
     gen = torch.Generator(device="cuda")
@@ -767,6 +812,10 @@ def main() -> int:
         log("leg q4_0 prefill (M=512)")
         out["prefill"] = leg_prefill(torch, args)
         log(f"prefill: {out['prefill']}")
+    if "geglu" in legs:
+        log("leg geglu -> q8_0 producer")
+        out["geglu"] = leg_geglu(torch, args)
+        log(f"geglu: {out['geglu']}")
     if "cfg1" in legs:
         log("leg cfg1")
         out["cfg1"] = leg_cfg1(torch, args)
@@ -828,6 +877,7 @@ def main() -> int:
         "w8a8": out.get("w8a8"),
         "w8a8_gemv": out.get("gemv"),
         "q4_0_prefill": out.get("prefill"),
+        "geglu_q8_0": out.get("geglu"),
         "w8a8_cpu_baseline": cpu_w8a8,
         "decode": decode,
         "configs": {key: out[key] for key in ("cfg0", "cfg1", "cfg2") if key in out},

@@ -137,6 +137,32 @@ int qxt_quantize_rows_int8(const float *x, size_t x_row_stride, int8_t *q, size_
 int qxt_quantize_q4_0(const float *w, size_t w_row_stride, void *blocks, size_t blocks_row_stride,
                       uint32_t rows, uint32_t columns, void *stream);
 
+/* ------------------------------------------------------ GEGLU -> Q8_0 producer */
+
+/* Host-only: fill table[65536] with GGML's exact-GELU fp16 lookup table, entry
+ * i = fp16(fl32(0.5 x (1 + erf(x / sqrt 2)))) for x = the fp16 value with bits
+ * i, the GELU evaluated in double.  Replaces ggml_gelu_fp16_table
+ * (src/qpu_xla/kernels/ggml_geglu_q8.py:26-34).  No device work. */
+int qxt_ggml_gelu_fp16_table(uint16_t *table);
+
+/* fp32 gate, up [rows, columns] -> native Q8_0 blocks u8 [rows, columns/32, 34] of
+ * v = fl32(table[fp16(gate)] * up) (fp16 RNE of the gate indexes the device copy of
+ * qxt_ggml_gelu_fp16_table), quantised as qxt_quantize_q8_0.  columns % 32 == 0.
+ * Replaces GGML_GEGLU_Q8_0_KERNEL (src/qpu_xla/kernels/ggml_geglu_q8.py:262-308),
+ * bit-identical to ggml_geglu_q8_0_reference (ggml_geglu_q8.py:37-59). */
+int qxt_ggml_geglu_q8_0(const float *gate, size_t gate_row_stride, const float *up, size_t up_row_stride,
+                        const uint16_t *gelu_table, void *blocks, size_t blocks_row_stride, uint32_t rows,
+                        uint32_t columns, void *stream);
+
+/* As qxt_ggml_geglu_q8_0, written as split planes for the tiled linear: int8
+ * values[rows, columns] and fp16 scale bits scales[rows, columns/32] held in
+ * scale_bytes = 2 (u16) or 4 (u32, zero-extended, the reference's layout) bytes.
+ * Replaces GGML_GEGLU_Q8_0_SPLIT_KERNEL (ggml_geglu_q8.py:311-385). */
+int qxt_ggml_geglu_q8_0_split(const float *gate, size_t gate_row_stride, const float *up, size_t up_row_stride,
+                              const uint16_t *gelu_table, void *scales, size_t scales_row_stride,
+                              uint32_t scale_bytes, int8_t *values, size_t values_row_stride, uint32_t rows,
+                              uint32_t columns, void *stream);
+
 /* -------------------------------------------------------- Q4_0 x Q8_0 linear */
 
 /* destination[r, output_column_start + j] =

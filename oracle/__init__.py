@@ -38,6 +38,17 @@ Pinning status (what each function is checked against, in ``tests/``):
 * ``pack_q4_0_lanes``: exact inversion and the byte position of every
   16-byte chunk (a layout of this library, checked against its definition
   chunk by chunk; the kernels' parity is then pinned by the linear's oracle).
+* ``gelu_fp16_table``: every entry against the same two roundings of an
+  independent erf (SciPy's), textbook values of the normal CDF
+  (x * Phi(x) at x = +-1, +-2, +-3), gelu(x) = x exactly for large x and the
+  odd-part identity gelu(x) - gelu(-x) = x within fp16 rounding.
+* ``geglu_q8_0_reference`` / ``geglu_q8_0_split_reference``: the reference's
+  own layout test (tests/test_qpu_xla_ggml_geglu_q8.py:24-30); the fp16
+  table index checked against torch's half conversion on exact fp16 ties;
+  cases that reduce to the pinned Q8_0 quantiser (up = 1 with gates where
+  gelu is the identity or exactly zero); dequantised blocks within half a
+  step of gelu(gate) * up computed in float64; the split planes against the
+  native blocks byte for byte.
 * ``quantize_q4_0_blocks``: PARITY UNPINNED against upstream ggml
   ``quantize_row_q4_0`` (ggml is not vendored in the reference); only the
   BASELINE formula's invariants are checked.
@@ -48,6 +59,10 @@ from oracle.ggml import (  # noqa: F401
     Q8_0_BLOCK_BYTES,
     QK,
     deinterleave_q8_0x4,
+    gelu_fp16_table,
+    geglu_activate,
+    geglu_q8_0_reference,
+    geglu_q8_0_split_reference,
     interleave_q8_0x4,
     pack_q4_0_blocks,
     pack_q4_0_lanes,

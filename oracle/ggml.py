@@ -12,6 +12,9 @@ Block formats (reference ``src/qpu_xla/kernels/ggml_q4_0.py:21-25``):
 
 from __future__ import annotations
 
+import math
+from functools import lru_cache
+
 import numpy as np
 
 QK = 32
@@ -391,3 +394,68 @@ def q8_0_q8_0_reference(activation_blocks: np.ndarray, weight_blocks: np.ndarray
         term *= dw[None, :, b]
         result += term
     return result
+
+
+# ------------------------------------------------------------ GEGLU -> Q8_0
+
+
+def gelu_fp16_table() -> np.ndarray:
+    """GGML's exact-GELU fp16 lookup table, u16 [65536] (a fresh copy per call).
+
+    Follows ``ggml_gelu_fp16_table`` (``src/qpu_xla/kernels/ggml_geglu_q8.py:26-34``):
+    entry ``i`` is ``0.5 x (1 + erf(x / sqrt 2))`` for ``x`` = the fp16 value
+    with bits ``i``, evaluated in Python double arithmetic, stored into a
+    float32 array (first rounding), then converted to float16 (second
+    rounding, both to nearest even).
+    """
+    return _gelu_fp16_table().copy()
+
+
+@lru_cache(maxsize=1)
+def _gelu_fp16_table() -> np.ndarray:
+    inputs = np.arange(1 << 16, dtype=np.uint16).view(np.float16).astype(np.float32)
+    out = np.empty_like(inputs)
+    root2 = math.sqrt(2.0)
+    with np.errstate(invalid="ignore"):
+        for index, value in enumerate(inputs):
+            x = float(value)
+            out[index] = 0.5 * x * (1.0 + math.erf(x / root2))
+        table = np.ascontiguousarray(out.astype(np.float16).view(np.uint16))
+    table.flags.writeable = False
+    return table
+
+
+def geglu_activate(gate: np.ndarray, up: np.ndarray, table: np.ndarray | None = None) -> np.ndarray:
+    """``fl32(table[fp16(gate)] * up)``, fp32 [M, K] (``ggml_geglu_q8.py:46-48``)."""
+    gate = np.asarray(gate, dtype=np.float32)
+    up = np.asarray(up, dtype=np.float32)
+    if gate.shape != up.shape or gate.ndim != 2 or gate.shape[1] % QK:
+        raise ValueError("gate/up must be equal rank-two F32 arrays with K divisible by 32")
+    lut = (_gelu_fp16_table() if table is None else np.asarray(table, dtype=np.uint16)).view(np.float16)
+    with np.errstate(invalid="ignore", over="ignore"):
+        return lut[gate.astype(np.float16).view(np.uint16)].astype(np.float32) * up
+
+
+def geglu_q8_0_reference(gate: np.ndarray, up: np.ndarray, table: np.ndarray | None = None) -> np.ndarray:
+    """Table GEGLU quantised straight to native Q8_0 blocks u8 [M, K/32, 34].
+
+    Follows ``ggml_geglu_q8_0_reference`` (``src/qpu_xla/kernels/ggml_geglu_q8.py:37-59``):
+    the activation of :func:`geglu_activate`, then per 32-element block
+    ``d = fl32(absmax / 127)``, ``inverse = fl32(1 / d)`` (0 when d == 0),
+    ``q = clip(rint(v * inverse), +-127)``, ``d`` stored as fp16 -- the rule
+    of :func:`quantize_q8_0_split`, applied here to the activation.
+    """
+    return quantize_q8_0_blocks(geglu_activate(gate, up, table))
+
+
+def geglu_q8_0_split_reference(
+    gate: np.ndarray, up: np.ndarray, table: np.ndarray | None = None
+) -> tuple[np.ndarray, np.ndarray]:
+    """Split planes of :func:`geglu_q8_0_reference`: (scale words u32 [M, K/32], values int8 [M, K]).
+
+    The scale word is the fp16 bits zero-extended, as the reference's split
+    producer stores it (``ggml_geglu_q8.py:186-192``) and its test reads it
+    (``tests/test_qpu_xla_ggml_geglu_q8.py:126-133``).
+    """
+    scale_bits, values = quantize_q8_0_split(geglu_activate(gate, up, table))
+    return scale_bits.astype(np.uint32), values

@@ -160,6 +160,9 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "qxt_quantize_q8_0": (c_int, [_P, _SZ, _P, _SZ, _U, _U, _P]),
     "qxt_quantize_rows_int8": (c_int, [_P, _SZ, _P, _SZ, _P, _U, _U, _U, _U, _P]),
     "qxt_quantize_q4_0": (c_int, [_P, _SZ, _P, _SZ, _U, _U, _P]),
+    "qxt_ggml_gelu_fp16_table": (c_int, [_P]),
+    "qxt_ggml_geglu_q8_0": (c_int, [_P, _SZ, _P, _SZ, _P, _P, _SZ, _U, _U, _P]),
+    "qxt_ggml_geglu_q8_0_split": (c_int, [_P, _SZ, _P, _SZ, _P, _P, _SZ, _U, _P, _SZ, _U, _U, _P]),
     "qxt_ggml_q4_0_q8_0_linear": (c_int, [_P, _SZ, _P, _SZ, _P, _SZ, _U, _U, _U, _U, _U, _P]),
     "qxt_ggml_q4_0_q8_0_block_dots": (c_int, [_P, _SZ, _P, _SZ, _P, _U, _U, _U, _U, _P]),
     "qxt_ggml_q8_0_q8_0_linear": (c_int, [_P, _SZ, _P, _SZ, _P, _SZ, _U, _U, _U, _U, _U, _P]),

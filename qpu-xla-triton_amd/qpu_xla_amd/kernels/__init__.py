@@ -11,6 +11,15 @@ from qpu_xla_amd.kernels.gemm_int8 import (  # noqa: F401
     w8a8_gemm_i32,
 )
 from qpu_xla_amd.kernels.gemv_int8 import W8A8_GEMV_KERNEL, supports_w8a8_gemv  # noqa: F401
+from qpu_xla_amd.kernels.ggml_geglu_q8 import (  # noqa: F401
+    GGML_GEGLU_Q8_0_KERNEL,
+    GGML_GEGLU_Q8_0_SPLIT_KERNEL,
+    ggml_geglu_q8_0,
+    ggml_geglu_q8_0_split,
+    ggml_gelu_fp16_table,
+    supports_ggml_geglu_q8_0,
+    supports_ggml_geglu_q8_0_split,
+)
 from qpu_xla_amd.kernels.ggml_q4_0 import (  # noqa: F401
     GGML_Q4_0_Q8_0_LINEAR_KERNEL,
     GGML_Q4_0_Q8_0_TILED_LINEAR_KERNEL,

@@ -82,6 +82,13 @@ FAKE = ctypes.c_void_p(1 << 20)  # 16-byte aligned, never dereferenced: validati
         ("qxt_w8a8_gemm_i32", (FAKE, 2**20, FAKE, 2**20, FAKE, 2**20, 16, 16, 140000, 0, None), "overflow"),
         ("qxt_w8a8_gemm_dequantize", (FAKE, 16, FAKE, 16, None, FAKE, None, FAKE, 64, 16, 16, 16, 0, None), "null"),
         ("qxt_w8a8_dequantize", (FAKE, 64, FAKE, FAKE, None, FAKE, 32, 1, 16, None), "stride"),
+        ("qxt_ggml_gelu_fp16_table", (None,), "null pointer"),
+        ("qxt_ggml_geglu_q8_0", (FAKE, 256, FAKE, 256, None, FAKE, 68, 1, 64, None), "null pointer"),
+        ("qxt_ggml_geglu_q8_0", (FAKE, 256, FAKE, 256, FAKE, FAKE, 68, 1, 48, None), "multiple of 32"),
+        ("qxt_ggml_geglu_q8_0", (FAKE, 256, FAKE, 128, FAKE, FAKE, 68, 2, 64, None), "strides"),
+        ("qxt_ggml_geglu_q8_0", (FAKE, 256, FAKE, 256, FAKE, FAKE, 67, 1, 64, None), "block stride"),
+        ("qxt_ggml_geglu_q8_0_split", (FAKE, 256, FAKE, 256, FAKE, FAKE, 8, 3, FAKE, 64, 1, 64, None), "scale_bytes"),
+        ("qxt_ggml_geglu_q8_0_split", (FAKE, 256, FAKE, 256, FAKE, FAKE, 8, 4, FAKE, 62, 1, 64, None), "strides"),
     ],
 )
 def test_invalid_arguments_are_rejected_on_the_host(name, args, fragment) -> None:
@@ -98,6 +105,8 @@ def test_injected_submission_failure_returns_before_launch() -> None:
         assert status == _lib.SUBMISSION_FAILED
         assert "injected" in _lib.last_error()
         status = lib.qxt_w8a8_gemm_i32(FAKE, 16, FAKE, 16, FAKE, 64, 16, 16, 16, 0, None)
+        assert status == _lib.SUBMISSION_FAILED
+        status = lib.qxt_ggml_geglu_q8_0(FAKE, 256, FAKE, 256, FAKE, FAKE, 68, 1, 64, None)
         assert status == _lib.SUBMISSION_FAILED
     finally:
         _lib.set_failure_mask(_lib.FAIL_NONE)
