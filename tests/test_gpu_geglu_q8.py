@@ -110,20 +110,30 @@ def test_random_shapes_bit_exact(rows: int, columns: int, sigma: float) -> None:
         np.testing.assert_array_equal(values.cpu().numpy(), planes)
 
 
-def test_every_fp16_gate_value() -> None:
-    # Every finite fp16 value as a gate (the full table through the kernel's
-    # index path), with up = 1 and with random up.
+BAND_MIN_BLOCKS = 1 << 16  # jobs of at least this many blocks take the LDS-band kernel
+
+
+@pytest.mark.parametrize("copies", [1, 34])  # 1: global-table kernel; 34 copies: >= 65536 blocks, LDS band
+def test_every_fp16_gate_value(copies: int) -> None:
+    # Every finite fp16 value as a gate (the whole table through the kernel's
+    # lookup path), with up = 1 and with random up, in rows of 1024 gates.
     bits = np.arange(1 << 16, dtype=np.uint16)
     finite = np.isfinite(bits.view(np.float16))
-    values = bits[finite].view(np.float16).astype(np.float32)
-    values = values[: values.size // 32 * 32].reshape(-1, 32)
-    rng = np.random.default_rng(5200)
+    values = np.tile(bits[finite].view(np.float16).astype(np.float32), copies)
+    values = values[: values.size // 1024 * 1024].reshape(-1, 1024)
+    assert (values.size // 32 >= BAND_MIN_BLOCKS) == (copies > 1)
+    rng = np.random.default_rng(5200 + copies)
     table = geglu.ggml_gelu_fp16_table("cuda")
     for up in (np.ones_like(values), rng.normal(0.0, 1.0, size=values.shape).astype(np.float32)):
         expected = oracle.geglu_q8_0_reference(values, up)
         actual = geglu.ggml_geglu_q8_0(dev(values), dev(up), table)
         torch.cuda.synchronize()
         np.testing.assert_array_equal(host_u8(actual), expected)
+    scales, planes = geglu.ggml_geglu_q8_0_split(dev(values), dev(up), table)
+    torch.cuda.synchronize()
+    words, expected_planes = oracle.geglu_q8_0_split_reference(values, up)
+    np.testing.assert_array_equal(scales.cpu().numpy().view(np.uint32), words)
+    np.testing.assert_array_equal(planes.cpu().numpy(), expected_planes)
 
 
 def test_fp16_ties_subnormals_and_zero_blocks() -> None:
@@ -155,6 +165,35 @@ def test_strided_unaligned_rows_and_destination() -> None:
     got = host_u8(out_full)
     np.testing.assert_array_equal(got[:, 1:4], expected)
     assert np.all(got[:, 0] == 0xEE)
+
+
+def test_band_kernel_strided_rows_and_misaligned_table() -> None:
+    # A job above the band threshold with rows at a 4-byte offset (scalar
+    # loads) and strided destination rows; then the same job with a table
+    # that is only 2-byte aligned, which the band kernel cannot copy with
+    # 16-byte loads and leaves to the global-table kernel.
+    rows, columns = 520, 4096
+    assert rows * columns // 32 >= BAND_MIN_BLOCKS
+    gate_full, up_full = gate_up(5204, rows, columns + 4, 1.2)
+    gate, up = gate_full[:, 1:columns + 1], up_full[:, 1:columns + 1]
+    expected = oracle.geglu_q8_0_reference(gate, up)
+    out_full = torch.full((rows, columns // 32 + 1, 34), 0xEE, dtype=torch.uint8, device="cuda")
+    geglu.ggml_geglu_q8_0(dev(gate_full)[:, 1:columns + 1], dev(up_full)[:, 1:columns + 1],
+                          destination=out_full[:, 1:])
+    torch.cuda.synchronize()
+    got = host_u8(out_full)
+    np.testing.assert_array_equal(got[:, 1:], expected)
+    assert np.all(got[:, 0] == 0xEE)
+    padded = torch.zeros(TABLE_PAD + (1 << 16), dtype=torch.int16, device="cuda")
+    padded[TABLE_PAD:] = geglu.ggml_gelu_fp16_table("cuda").view(torch.int16)
+    table = padded[TABLE_PAD:].view(torch.uint16)
+    assert table.data_ptr() % 16 == 2
+    actual = geglu.ggml_geglu_q8_0(dev(gate), dev(up), table)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host_u8(actual), expected)
+
+
+TABLE_PAD = 1  # one int16 in front of the table: its data pointer is 2 mod 16
 
 
 def test_kernel_contract_checks() -> None:

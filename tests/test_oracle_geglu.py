@@ -71,6 +71,18 @@ def test_table_identities() -> None:
     assert table[0] == 0.0
 
 
+def test_closed_forms_outside_the_lds_band() -> None:
+    # The band kernel keeps fp16 magnitudes in [2^-10, 8) in LDS and uses
+    # closed forms beyond: gelu(x) = x for finite x >= 8, -0 for finite x <= -8.
+    table = oracle.gelu_fp16_table()
+    magnitude = FP16_BITS & 0x7FFF
+    beyond = (magnitude >= 0x4800) & (magnitude < 0x7C00)
+    positive = beyond & (FP16_BITS < 0x8000)
+    negative = beyond & (FP16_BITS >= 0x8000)
+    np.testing.assert_array_equal(table[positive], FP16_BITS[positive])
+    assert np.all(table[negative] == 0x8000)
+
+
 def test_library_table_equals_oracle() -> None:
     from qpu_xla_amd import _lib
     from qpu_xla_amd.kernels import ggml_gelu_fp16_table
