@@ -42,6 +42,14 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source additions.  The prefill kernel converts every matrix-core result
+# with VALU instructions, so its MFMAs write VGPRs directly (no accumulator-
+# register copies); the W8A8 GEMM keeps its 256 accumulators in AGPRs.
+SOURCE_FLAGS = {
+    "qxt_q4_0_tiled.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _hipcc() -> str:
     found = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(found).exists():
@@ -67,8 +75,8 @@ def source_hash() -> str:
 
 def _compile(source: Path, defines: tuple[str, ...] = ()) -> Path:
     obj = BUILD_DIR / (source.stem + ".o")
-    cmd = [_hipcc(), *HIPCC_FLAGS, *defines, "-I", str(REPO_ROOT / "include"), "-I", str(CSRC), "-c", str(source),
-           "-o", str(obj)]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(source.name, []), *defines, "-I", str(REPO_ROOT / "include"),
+           "-I", str(CSRC), "-c", str(source), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed on {source.name}:\n{proc.stderr}")
