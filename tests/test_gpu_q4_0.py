@@ -317,11 +317,18 @@ def test_tiled_linear_shapes_bit_exact_and_device_packing(rows: int, blocks: int
     np.testing.assert_array_equal(out, expected)
 
 
-@pytest.mark.parametrize("rows,blocks,wcol0,ncols", [(16, 8, 0, 48), (33, 5, 3, 61), (100, 12, 0, 128), (64, 1, 16, 16)])
+@pytest.mark.parametrize("rows,blocks,wcol0,ncols", [
+    (16, 8, 0, 48), (33, 5, 3, 61), (100, 12, 0, 128), (64, 1, 16, 16),
+    (33, 5, 3, 60),  # the last activation block and the last weight block both end 2 bytes into a dword
+    (530, 176, 0, 200),  # several staged groups, a ragged last row tile
+])
 def test_native_linear_prefill_rows_run_on_matrix_cores_bit_exact(rows: int, blocks: int, wcol0: int, ncols: int) -> None:
     # rows >= 16 through the native-layout entry point: odd block counts give
     # activation rows that are not 4-byte aligned; a column partition with a
-    # sentinel prefix checks that only the requested columns are written.
+    # sentinel prefix checks that only the requested columns are written.  A
+    # block whose 32 values (or 16 nibble bytes) start 2 bytes into a dword
+    # needs 2 bytes of the dword after them; when that block ends the tensor,
+    # the rest of that dword lies past the operand's range.
     act, wt = _split_case(5000 + rows + blocks, rows, blocks, wcol0 + ncols + 5)
     destination = torch.full((rows, ncols + 16), float(SENTINEL), device="cuda")
     q4.ggml_q4_0_q8_0_linear(dev(act), dev(wt), destination, weight_column_start=wcol0,
