@@ -248,16 +248,17 @@ __global__ __launch_bounds__(kThreads) void q4_0_tiled_kernel(TiledArgs t) {
 //
 // Native fragments sit at 2-byte offsets, one scattered row per lane, so a
 // workgroup stages kGroup blocks at a time of its 64 activation rows and 64
-// weight columns in LDS instead: 8 consecutive threads read the 8
+// weight columns in LDS instead: kGroup consecutive threads read the
 // consecutive blocks of one row (contiguous bytes), realign them and convert
 // the weight nibbles to int8 once per workgroup, and write per row (column)
 // kGroup runs of 32 signed bytes in k order, rows padded to kPitch bytes,
 // plus fp32 scales.  Global loads are issued a group ahead into registers and
 // written to the other of two LDS buffers at the end of the current group
 // (one barrier per group); the waves read 16-byte aligned fragments.
-constexpr int kGroup = 8;                          // blocks per staged group
+constexpr int kGroup = 4;                          // blocks per staged group (8: 10 % slower at M = 512)
 constexpr int kPitch = kGroup * 32 + 16;           // bytes per staged row (padding spreads banks)
-constexpr int kPairs = kTile * kGroup / kThreads;  // (row, block) pairs per thread per operand: 2
+constexpr int kPairs = kTile * kGroup / kThreads;  // (row, block) pairs per thread per operand
+static_assert(kPairs >= 1 && kGroup % 4 == 0, "a group is staged by whole pairs and scaled 4 blocks at a time");
 
 struct StageBuf {
     uint8_t a[kTile * kPitch];
@@ -464,7 +465,7 @@ int launch_tiled(const TiledArgs &t, bool native, hipStream_t stream) {
     // Native 18/34-byte blocks are staged through LDS by the workgroup (their
     // fragments sit at 2-byte offsets, one scattered row per lane); the split
     // planes are read as fragments directly (measured on MI355X at M = 512:
-    // native gate_up 103 -> 45 us staged; split 43 us direct, 64 us staged).
+    // native gate_up 103 -> 42 us staged; split 44 us direct, 64 us staged).
     if (native) return launch("q4_0_tiled_kernel", q4_0_staged_kernel, grid, dim3(kThreads), 0, stream, t);
     return launch("q4_0_tiled_kernel", q4_0_tiled_kernel, grid, dim3(kThreads), 0, stream, t);
 }
