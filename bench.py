@@ -748,6 +748,71 @@ def cpu_baseline_w8a8(budget_s: float) -> dict:
     }
 
 
+def _blas_threads() -> int | None:
+    """Threads of NumPy's BLAS (threadpoolctl), or None when it cannot tell."""
+    try:
+        from threadpoolctl import threadpool_info
+    except ImportError:
+        return None
+    counts = [pool.get("num_threads") for pool in threadpool_info() if pool.get("user_api") == "blas"]
+    return max(counts) if counts else None
+
+
+def cpu_references_w8a8(budget_s: float) -> dict:
+    """The reference benchmark's other CPU references on a row sample of cfg4 gate/up.
+
+    examples/benchmark_qpu_xla_w8a8.py:199-265: the dynamic W8A8 projection in
+    torch int32 (per-row activation quantisation, int32 matmul, fp32
+    scaling), and the unquantised fp32 projection in NumPy (BLAS) and torch.
+    Each is timed with 2 warm-up calls and up to 7 timed calls within its
+    share of ``budget_s``; ``threads`` is what the library used.
+    """
+    import oracle
+    import torch
+
+    rng = np.random.default_rng(4)
+    k, n = 4096, 14336
+    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    qw, sw = oracle.quantize_per_output_channel_int8(w)
+    torch_w32 = torch.from_numpy(qw.astype(np.int32))
+    torch_sw = torch.from_numpy(sw)
+    torch_w = torch.from_numpy(w)
+
+    def torch_int32(x):
+        t = torch.from_numpy(x)
+        sa = torch.maximum(torch.amax(torch.abs(t), dim=1) / 127, torch.tensor(1.0 / 127.0))
+        q = torch.round(t / sa[:, None]).clamp(-127, 127).to(torch.int32)
+        return (q @ torch_w32.T).to(torch.float32) * sa[:, None] * torch_sw[None, :]
+
+    cases = {
+        "torch_int32_w8a8": (16, torch_int32),
+        "numpy_fp32": (64, lambda x: x @ w.T),
+        "torch_fp32": (64, lambda x: torch.from_numpy(x) @ torch_w.T),
+    }
+    out = {}
+    for name, (rows, fn) in cases.items():
+        x = rng.standard_normal((rows, k), dtype=np.float32)
+        for _ in range(2):
+            fn(x)
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < 7 and time.perf_counter() - t_start < budget_s / len(cases):
+            t0 = time.perf_counter()
+            fn(x)
+            times.append(time.perf_counter() - t0)
+        best = min(times)
+        out[name] = {
+            "value": 2 * rows * n * k / best / 1e12,
+            "unit": "TOPS",
+            "rows": rows,
+            "shape": f"M={rows} K={k} N={n}",
+            "calls": len(times),
+            "best_ms": best * 1e3,
+            "threads": torch.get_num_threads() if name.startswith("torch") else _blas_threads(),
+        }
+    return out
+
+
 def measured_traffic(kernel: str) -> dict | None:
     """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH/WRITE summary, if any."""
     path = ROOT / "profiles" / f"{kernel}_cfg3_traffic.json"
@@ -769,6 +834,17 @@ def host_info() -> dict:
         pass
     for var in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS"):
         info[var] = os.environ.get(var)
+    try:
+        import torch
+
+        info["torch_threads"] = torch.get_num_threads()
+    except ImportError:
+        pass
+    try:
+        blas = np.show_config(mode="dicts").get("Build Dependencies", {}).get("blas", {})
+        info["numpy_blas"] = f"{blas.get('name')} {blas.get('version')}"
+    except (TypeError, AttributeError):
+        pass
     try:
         with open("/proc/cpuinfo") as fh:
             for line in fh:
@@ -847,6 +923,7 @@ def main() -> int:
         log("cpu baseline (NumPy oracle)")
         cpu = cpu_baseline_q4(args.cpu_seconds)
         cpu_w8a8 = cpu_baseline_w8a8(args.cpu_seconds)
+        cpu_w8a8["reference_cpu_paths"] = cpu_references_w8a8(args.cpu_seconds)
         cpu["host"] = host_info()
         log(f"cpu: {cpu} / {cpu_w8a8}")
 
