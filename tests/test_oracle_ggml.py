@@ -2,6 +2,8 @@
 
 from __future__ import annotations
 
+from pathlib import Path
+
 import numpy as np
 import pytest
 
@@ -338,3 +340,20 @@ def test_q8_0_reference_scales_by_the_activation_first() -> None:
             assert oracle.q8_0_q8_0_reference(act, wt)[0, 0] == a_first
             return
     pytest.fail("no order-sensitive case found")
+
+
+def test_real_activation_fixture_quantises_within_the_q8_0_invariants() -> None:
+    # tests/golden/mtp_activation.f32: the reference's captured K=256 activation
+    # (artifact/evidence/mtp/activation.f32), 256 little-endian fp32 values.
+    x = np.fromfile(Path(__file__).resolve().parent / "golden" / "mtp_activation.f32", dtype="<f4")
+    assert x.shape == (256,) and np.all(np.isfinite(x))
+    scale_bits, codes = oracle.quantize_q8_0_split(x.reshape(1, 256))
+    d = scale_bits.view(np.float16).astype(np.float32).reshape(8)
+    blocks = x.reshape(8, 32)
+    q = codes.reshape(8, 32).astype(np.int32)
+    assert np.all(np.abs(q) <= 127)
+    # the absmax element of every block maps to +-127 and the reconstruction is within half a step
+    assert np.all(np.abs(q[np.arange(8), np.argmax(np.abs(blocks), axis=1)]) == 127)
+    step = np.abs(blocks).max(axis=1) / 127
+    assert np.all(np.abs(blocks - q * step[:, None]) <= 0.5 * step[:, None] * (1 + 1e-6))
+    np.testing.assert_allclose(d, (np.abs(blocks).max(axis=1) / np.float32(127)).astype(np.float16), rtol=0)
