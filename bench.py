@@ -17,7 +17,7 @@ Also reported on the same JSON line:
   * ``configs``       -- cfg0 (rotated over >= 512 MB of weight copies), cfg1, cfg2;
   * ``cpu_baseline``  -- the NumPy oracle of the reference CPU path on this host.
 
-Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--legs decode,w8a8,gemv,prefill,geglu,cfg0,cfg1,cfg2,copy,cpu]
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--legs decode,w8a8,gemv,prefill,geglu,shards,cfg0,cfg1,cfg2,copy,cpu]
 Weights and activations are synthetic (seeded random, the BASELINE distributions).
 """
 
@@ -68,7 +68,7 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--legs", default="decode,w8a8,gemv,prefill,geglu,cfg0,cfg1,cfg2,copy,cpu")
+    ap.add_argument("--legs", default="decode,w8a8,gemv,prefill,geglu,shards,cfg0,cfg1,cfg2,copy,cpu")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of each CPU-baseline sample")
     return ap.parse_args()
 
@@ -425,11 +425,12 @@ def _w8a8_operands(torch, gen, m: int, k: int, n: int):
     return x, weight, bias
 
 
-def leg_w8a8(torch, args) -> dict:
-    """cfg4: dynamic W8A8 prefill GEMMs at Llama-3-8B FFN shapes, M=4096."""
+def leg_w8a8(torch, args, shapes: dict | None = None) -> dict:
+    """cfg4: dynamic W8A8 prefill GEMMs at Llama-3-8B FFN shapes, M=4096 (or the given shapes)."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(4)
-    shapes = {"gate_up": (4096, 4096, 14336), "down": (4096, 14336, 4096)}
+    if shapes is None:
+        shapes = {"gate_up": (4096, 4096, 14336), "down": (4096, 14336, 4096)}
     result = {}
     total_ops = 0
     total_ms = 0.0
@@ -480,6 +481,20 @@ def leg_w8a8(torch, args) -> dict:
         "ops_per_launch": total_ops // 2,
     }
     return result
+
+
+def leg_shards(torch, args) -> dict:
+    """One GPU's share of the 8-GPU shardings the path would use (the collectives are not run).
+
+    Q4_0 shards by output columns (the reference's wcol0 / ocol0 / ncols
+    partition): cfg0's N = 5632 over 8 GPUs is N = 704 per GPU, rotated
+    weights.  W8A8 shards by rows with replicated weights: cfg4's M = 4096 over
+    8 GPUs is M = 512 per GPU at the full K and N.
+    """
+    return {
+        "q4_0_cfg0_column_shard": leg_rotated_q4(torch, args, 1, 2048, 704, 10),
+        "w8a8_cfg4_row_shard": leg_w8a8(torch, args, {"gate_up": (512, 4096, 14336), "down": (512, 14336, 4096)}),
+    }
 
 
 def leg_w8a8_gemv(torch, args) -> dict:
@@ -910,6 +925,10 @@ def main() -> int:
         log("leg geglu -> q8_0 producer")
         out["geglu"] = leg_geglu(torch, args)
         log(f"geglu: {out['geglu']}")
+    if "shards" in legs:
+        log("leg shards (one GPU's share of an 8-GPU sharding)")
+        out["shards"] = leg_shards(torch, args)
+        log(f"shards: {out['shards']}")
     if "cfg1" in legs:
         log("leg cfg1")
         out["cfg1"] = leg_cfg1(torch, args)
@@ -973,6 +992,7 @@ def main() -> int:
         "w8a8_gemv": out.get("gemv"),
         "q4_0_prefill": out.get("prefill"),
         "geglu_q8_0": out.get("geglu"),
+        "shards": out.get("shards"),
         "w8a8_cpu_baseline": cpu_w8a8,
         "decode": decode,
         "configs": {key: out[key] for key in ("cfg0", "cfg1", "cfg2") if key in out},

@@ -903,6 +903,15 @@ int run_gemm(const GemmArgs &args, int epi, uint32_t layout, hipStream_t stream)
         // full tile.)
         return launch_stream(args, epi, stream);
     }
+    // Fewer 128 x 128 tiles than CUs (small M and N, e.g. one GPU's row shard
+    // of a down projection, M = 512, N = 4096, K = 14336): 64 x 64 tiles with
+    // 128-byte K stages fill the GPU instead (measured on MI355X: 115 -> 69 us
+    // for that shard; 31 -> 17 us at M = 256, K = N = 4096).
+    const long t128 = ((args.m + 127) / 128) * ((args.n + 127) / 128);
+    if (!big && t128 < cus) {
+        if (layout == QXT_W8A8_WEIGHT_K4N) return launch_gemm<64, 64, 128, 1, 1, true>(args, epi, layout, stream);
+        return launch_gemm<64, 64, 128, 1, 1, false>(args, epi, layout, stream);
+    }
     if (layout == QXT_W8A8_WEIGHT_K4N)
         return big ? launch_gemm<256, 256, 128, D, S, true>(args, epi, layout, stream)
                    : launch_gemm<128, 128, 64, 1, 1, true>(args, epi, layout, stream);
