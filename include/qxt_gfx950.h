@@ -258,8 +258,10 @@ int qxt_ggml_q8_0_q8_0_linear(const void *activation, size_t activation_row_stri
                               uint32_t column_count, void *stream);
 
 /* One linear of a Q4_0 batch.  Exactly one of `x` (fp32 rows [rows, blocks*32]
- * with 16-byte aligned rows, quantised to Q8_0 by the rule of qxt_quantize_q8_0
- * in a pre-pass launch of the batch) and `activation` (native Q8_0 blocks) is non-NULL; the
+ * with 16-byte aligned rows, quantised to Q8_0 by the rule of qxt_quantize_q8_0:
+ * in a pre-pass launch of the batch when the batch has more than 1024 work
+ * items, else by every workgroup that reads them) and `activation` (native
+ * Q8_0 blocks) is non-NULL; the
  * other fields mean what they mean for qxt_ggml_q4_0_q8_0_linear.  Batched
  * tasks need rows <= 4, blocks % 8 == 0 and 16-byte aligned weight rows.
  * weight_layout QXT_Q4_0_LAYOUT_LANES: `weight` is the base of a
@@ -292,7 +294,8 @@ typedef struct qxt_q4_0_batch qxt_q4_0_batch;
 int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_batch **batch);
 
 /* Enqueue the whole batch on `stream`: the Q8_0 pre-pass (when a task has fp32
- * rows) and the batch grid, two launches; graph-capturable.
+ * rows and the batch has more than 1024 work items) and the batch grid;
+ * graph-capturable.
  * Replaces qpu_llama_q4_0_linear_submit (qpu_llama_q4_0.h:72-75). */
 int qxt_q4_0_batch_launch(const qxt_q4_0_batch *batch, void *stream);
 

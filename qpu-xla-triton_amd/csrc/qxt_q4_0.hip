@@ -59,7 +59,9 @@ constexpr int kThreads = 256;
 constexpr size_t kMaxLds = 64 * 1024;
 
 struct Q4Task {
-    const uint8_t *act;    // native Q8_0 blocks [rows, blocks, 34]
+    const float *x;        // fp32 rows quantised to Q8_0 in the workgroup, or nullptr
+    size_t x_stride;
+    const uint8_t *act;    // native Q8_0 blocks [rows, blocks, 34] (when x is nullptr)
     const uint8_t *w;      // Q4_0 blocks [N, blocks, 18]
     float *y;              // fp32 output
     int32_t *dots;         // debug: int32 block dots [rows, ncols, blocks]
@@ -138,6 +140,52 @@ __device__ __forceinline__ int block_dot(const uint32_t (&qs)[4], const int *aq,
 template <int MR>
 __device__ __forceinline__ void stage_activation(const Q4Task &t, int r0, int *aq, int *ad, const Q4Lds &geo) {
     const int B = t.blocks;
+    if (t.x != nullptr) {
+        // fp32 rows (a small batch, no pre-pass): quantised to Q8_0 by the
+        // rule of q8_0_prepass_kernel, 8 lanes per block and float4 per lane,
+        // four loads in flight per thread; the dots use the fp16-rounded d.
+        // `total` and every chunk start are multiples of 8, so the 8 lanes of
+        // a block are active together.
+        const int total = MR * B * 8;
+        for (int base = 0; base < total; base += 4 * kThreads) {
+            float4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int e = base + u * kThreads + threadIdx.x;
+                v[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                const int r = e / (B * 8);
+                if (e < total && r0 + r < t.rows)
+                    v[u] = *reinterpret_cast<const float4 *>(reinterpret_cast<const uint8_t *>(t.x) +
+                                                             (r0 + r) * t.x_stride + (e - r * B * 8) * 16);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int e = base + u * kThreads + threadIdx.x;
+                if (e >= total) break;
+                const int r = e / (B * 8);
+                const int rem = e - r * B * 8;
+                const int b = rem >> 3, l8 = rem & 7;
+                float amax = fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w)));
+                amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
+                amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
+                amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
+                const float d = amax / 127.0f;
+                const float inv = (d != 0.0f) ? 1.0f / d : 0.0f;
+                const int q0 = clamp127(rintf(v[u].x * inv)), q1 = clamp127(rintf(v[u].y * inv));
+                const int q2 = clamp127(rintf(v[u].z * inv)), q3 = clamp127(rintf(v[u].w * inv));
+                int sum = q0 + q1 + q2 + q3;
+                sum += __shfl_xor(sum, 1, 8);
+                sum += __shfl_xor(sum, 2, 8);
+                sum += __shfl_xor(sum, 4, 8);
+                aq[r * geo.aq_row + aq_index(b, l8)] = static_cast<int>(pack_bytes(q0, q1, q2, q3));
+                if (l8 == 0) {
+                    ad[r * geo.ad_row + ad_index(b)] = __float_as_int(half_bits_to_float(float_to_half_bits(d)));
+                    ad[r * geo.ad_row + ad_index(b) + 1] = sum;
+                }
+            }
+        }
+        return;
+    }
     for (int idx = threadIdx.x; idx < MR * B; idx += kThreads) {
         const int r = idx / B;
         const int b = idx - r * B;
@@ -220,6 +268,11 @@ __global__ __launch_bounds__(kThreads) void pack_lanes_kernel(const uint8_t *__r
 }
 
 // One fp32 activation of a batch to quantise: rows x blocks Q8_0 blocks.
+// Batches of at most this many work items quantise their fp32 activations
+// inside each workgroup instead of in a pre-pass launch (a decode step's
+// dependency stages: 128-704 items; the whole cfg3 step: 7436).
+constexpr size_t kFusedQuantItems = 1024;
+
 struct Q8Job {
     const float *x;
     size_t x_stride;
@@ -699,9 +752,12 @@ int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_
             return fail(QXT_INVALID_ARGUMENT, "q4_0 batch task %u: column range overflows", i);
         Q4Task t{};
         if (d.x != nullptr) {
-            // Quantised by the pre-pass into the batch's staging buffer (pointer patched below).
+            // Quantised by the pre-pass into the batch's staging buffer (pointer
+            // patched below), or by each workgroup in a small batch.
             jobs.push_back({d.x, d.x_row_stride, nullptr, static_cast<int>(d.rows), static_cast<int>(d.blocks)});
             job_task.push_back(i);
+            t.x = d.x;
+            t.x_stride = d.x_row_stride;
             t.act = nullptr;
             t.act_stride = static_cast<size_t>(d.blocks) * Q8_0_BYTES;
         } else {
@@ -736,6 +792,15 @@ int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_
             items.push_back({static_cast<int>(i), c, std::min(host[i].cpw, host[i].ncols - c)});
     }
     if (items.size() > 0x7FFFFFFFu) return fail(QXT_INVALID_ARGUMENT, "q4_0 batch: too many work items");
+    if (items.size() <= kFusedQuantItems) {
+        // Small batch: every workgroup quantises the rows it needs itself (an
+        // L2-resident re-read per workgroup) rather than waiting for a
+        // separate pre-pass launch.
+        jobs.clear();
+        job_task.clear();
+    } else {
+        for (uint32_t i : job_task) host[i].x = nullptr;
+    }
     std::vector<Q8Chunk> chunks;
     size_t staging_bytes = 0;
     std::vector<size_t> job_offset(jobs.size());
