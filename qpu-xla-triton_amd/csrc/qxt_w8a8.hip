@@ -200,18 +200,19 @@ __device__ __forceinline__ void store_tile(const GemmArgs &args, const v16i (&ac
     }
 }
 
-// Epilogue of a 256 x 256 tile held by four waves of 128 x 128 (waves 2 x 2),
-// staged through LDS so that global stores are whole 1 KB tile rows (16
-// bytes per lane) instead of 128-byte row pieces.  Two passes: in pass p
-// every wave writes its 32-row blocks i = 2p, 2p + 1 (tile rows
-// wm * 128 + 64p + [0, 64)) to `buf` row-major, then each wave stores 32 of
-// the 128 buffered rows.  Each accumulator is converted in exactly one pass.
-// Rows past M are skipped and columns past N masked (edge lanes and
+// Epilogue of a 256 x 256 tile held by eight waves of 128 x 64: wave w owns
+// tile rows (w & 3) / 2 * 128 + [0, 128) and columns ((w & 3) % 2) * 128 +
+// (w / 4) * 64 + [0, 64).  Staged through LDS so that global stores are whole
+// 1 KB tile rows (16 bytes per lane) instead of 128-byte row pieces.  Two
+// passes: in pass p every wave writes its 32-row blocks i = 2p, 2p + 1 (tile
+// rows wm * 128 + 64p + [0, 64)) to `buf` row-major, then each wave stores 16
+// of the 128 buffered rows.  Each accumulator is converted in exactly one
+// pass.  Rows past M are skipped and columns past N masked (edge lanes and
 // unaligned outputs store element by element).  `scales` holds what
 // stage_scales wrote; `buf` takes 128 KB.
 template <int EPI>
-__device__ __forceinline__ void store_tile_rows(const GemmArgs &args, const v16i (&acc)[4][4], int m0, int n0,
-                                                int wm, int wn, int lane, uint8_t *buf, const float *scales) {
+__device__ __forceinline__ void store_tile_rows(const GemmArgs &args, const v16i (&acc)[4][2], int m0, int n0,
+                                                int wm, int wcol, int lane, uint8_t *buf, const float *scales) {
     constexpr int BM = 256, BN = 256;
     const int hl = lane >> 5;
     const int wave = threadIdx.x >> 6;
@@ -224,8 +225,8 @@ __device__ __forceinline__ void store_tile_rows(const GemmArgs &args, const v16i
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int col = wn * 128 + j * 32 + (lane & 31);
+        for (int j = 0; j < 2; ++j) {
+            const int col = wcol + j * 32 + (lane & 31);
             float swn = 0.0f, bn = 0.0f;
             if constexpr (EPI != EPI_I32) {
                 swn = scales[BM + col];
@@ -258,12 +259,13 @@ __device__ __forceinline__ void store_tile_rows(const GemmArgs &args, const v16i
             }
         }
         __syncthreads();
-        // Lane l stores columns n0 + 4l .. 4l + 3 of each row: one 16-byte store
-        // when all four are inside N and the address is 16-byte aligned,
-        // otherwise element by element.
+        // Buffered row br holds tile row (br / 64) * 128 + 64p + br % 64.  Lane
+        // l stores columns n0 + 4l .. 4l + 3 of each row: one 16-byte store when
+        // all four are inside N and the address is 16-byte aligned, otherwise
+        // element by element.
 #pragma unroll 4
-        for (int t = 0; t < 32; ++t) {
-            const int br = wave * 32 + t;
+        for (int t = 0; t < 16; ++t) {
+            const int br = wave * 16 + t;
             const int gm = m0 + (br >> 6) * 128 + p * 64 + (br & 63);
             if (gm < args.m) {
                 const v4u v = *reinterpret_cast<const v4u *>(fb + br * BN + lane * 4);
@@ -284,16 +286,6 @@ __device__ __forceinline__ void store_tile_rows(const GemmArgs &args, const v16i
 // LDS bytes the 256 x 256 epilogue uses: the 128 KB half-tile buffer and
 // the staged scales behind it.
 constexpr int kEpilogueLds = 128 * 1024 + 3 * 256 * 4;
-
-// Epilogue of the 256 x 256 kernels (LDS free, all waves past their last
-// LDS read).
-template <int EPI>
-__device__ __forceinline__ void epilogue_256(const GemmArgs &args, const v16i (&acc)[4][4], int m0, int n0, int wm,
-                                             int wn, int lane, uint8_t *smem) {
-    float *scales = reinterpret_cast<float *>(smem + 128 * 1024);
-    stage_scales<256, 256, EPI>(args, scales, m0, n0);
-    store_tile_rows<EPI>(args, acc, m0, n0, wm, wn, lane, smem, scales);
-}
 
 // BM x BN output tile per 256-thread workgroup; waves 2 x 2, each (BM/2) x (BN/2)
 // as (BM/64) x (BN/64) blocks of 32 x 32.  K advances BKT bytes per stage
@@ -409,34 +401,39 @@ __global__ __launch_bounds__(kThreads) void w8a8_gemm_kernel(GemmArgs args) {
 
 // ----------------------------------------------------------------------------
 // Large-tile streaming kernel for the common case: weight layout [N, K],
-// K % 128 == 0.  256 x 256 x 128 stages, two register stages in flight, and
-// every k step of a stage issues its memory work one instruction per MFMA:
-// 8 fragment reads of the next k step, 4 LDS writes of stage s+1 (loaded a
-// full stage earlier) and 4 global loads of stage s+2 between 16 MFMAs, so
-// the single wave per SIMD never stops feeding the matrix pipe for long.
-// Rows past M or N need no predicate: their offsets fall outside the
-// buffer descriptor's range and load zeros.  Output tiles are mapped to
-// workgroups XCD by XCD (xcd_tile) and written through LDS one tile row per
-// store (store_tile_rows).
+// K % 128 == 0.  A 256 x 256 output tile per workgroup of eight waves, two
+// per SIMD (waves w and w + 4 share SIMD w % 4), each wave a 128 x 64
+// sub-tile of 4 x 2 blocks of 32 x 32 (128 accumulators), so that while one
+// wave of a SIMD waits on LDS or memory the other keeps the matrix pipe fed.
+// K advances in 128-byte stages through two LDS buffers, two register stages
+// in flight: every k step issues, between its 8 MFMAs, the 6 fragment reads
+// of the next k step, 2 LDS writes of stage s+1 (loaded a full stage
+// earlier) and 2 global loads of stage s+2.  Rows past M or N need no
+// predicate: their offsets fall outside the buffer descriptor's range and
+// load zeros.  Output tiles are mapped to workgroups XCD by XCD (xcd_tile)
+// and written through LDS one tile row per store (store_tile_rows).
 //
-// Measured alternatives on MI355X (cfg4 shapes, realistic operand values):
-// the same tiling with operands loaded by LDS DMA (buffer_load ... lds, a
-// four-stage ring of 64-byte K stages, XOR-swizzled rows) was no faster
-// (within +-5 %), and no buffer-load cache policy changed the main loop by
-// more than noise; skipping the global loads altogether (a timing-only
-// variant) speeds the main loop up by ~1.4x, so L2 -> CU operand traffic, not
-// instruction issue, bounds it.
+// Measured on MI355X (cfg4 shapes, interleaved runs in one process): against
+// four waves of 128 x 128 (one wave per SIMD, the same stages) this runs
+// gate_up in 240 us instead of 258 us and down in 206 us instead of 208 us;
+// the matrix pipes are busier (52 / 67 % against 46 / 63 %) while the board
+// lowers the clock (1.80 / 1.69 GHz against 1.90 / 1.77 GHz in the same
+// profiling session), i.e. power bounds both.  Grouping each k step's MFMAs
+// into one burst (with or without a raised wave priority) or leaving the
+// placement to the compiler was 1-4 % slower.
 namespace big {
+constexpr int THREADS = 512;
 constexpr int BM = 256, BN = 256, BKT = 128;
 constexpr int ROW = BKT + 16;              // LDS row pitch (bytes)
 constexpr int STAGE = (BM + BN) * ROW;     // one LDS buffer (A then B)
 constexpr int CPR = BKT / 16;              // 16-byte chunks per row
-constexpr int RPI = kThreads / CPR;        // rows covered by one load instruction
-constexpr int A_CHUNKS = BM / RPI;         // 8
-constexpr int B_CHUNKS = BN / RPI;         // 8
+constexpr int RPI = THREADS / CPR;         // rows covered by one load instruction
+constexpr int A_CHUNKS = BM / RPI;         // 4
+constexpr int B_CHUNKS = BN / RPI;         // 4
+constexpr int Q = A_CHUNKS + B_CHUNKS;     // 16-byte chunks per thread per stage
 constexpr int KSTEPS = BKT / 32;           // 4
-constexpr int TM = 4, TN = 4;              // 32x32 blocks per wave (128 x 128)
-constexpr int PER_STEP = (A_CHUNKS + B_CHUNKS) / KSTEPS;  // loads (and writes) per k step
+constexpr int TM = 4, TN = 2;              // 32x32 blocks per wave (128 x 64)
+constexpr int PER_STEP = Q / KSTEPS;       // loads (and writes) per k step
 static_assert(2 * STAGE >= kEpilogueLds, "the epilogue reuses the operand buffers");
 }  // namespace big
 
@@ -461,12 +458,13 @@ __device__ __forceinline__ void xcd_tile(int pid, int tm, int tn, int gm, int &t
 }
 
 template <int EPI>
-__global__ __launch_bounds__(kThreads) void w8a8_gemm_stream_kernel(GemmArgs args) {
+__global__ __launch_bounds__(big::THREADS) void w8a8_gemm_stream_kernel(GemmArgs args) {
     using namespace big;
     __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = (wave & 3) >> 1;                    // 128-row half of the tile
+    const int wcol = (wave & 1) * 128 + (wave >> 2) * 64;  // first of the wave's 64 columns
     int ty, tx;
     xcd_tile(blockIdx.x, (args.m + BM - 1) / BM, (args.n + BN - 1) / BN, 4, ty, tx);
     const int m0 = ty * BM;
@@ -490,16 +488,18 @@ __global__ __launch_bounds__(kThreads) void w8a8_gemm_stream_kernel(GemmArgs arg
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
     const int a_lane = (wm * 128 + (lane & 31)) * ROW + (lane >> 5) * 16;
-    const int b_lane = (wn * 128 + (lane & 31)) * ROW + (lane >> 5) * 16;
+    const int b_lane = (wcol + (lane & 31)) * ROW + (lane >> 5) * 16;
     v4i af[2][TM], bf[2][TN];
+    // Fragments in the order the MFMAs of a k step consume them.
     auto read_frags = [&](const uint8_t *As, int kk, int buf) {
         const uint8_t *Bs = As + BM * ROW;
-#pragma unroll
-        for (int i = 0; i < TM; ++i) af[buf][i] = *reinterpret_cast<const v4i *>(As + a_lane + i * 32 * ROW + kk);
+        af[buf][0] = *reinterpret_cast<const v4i *>(As + a_lane + kk);
 #pragma unroll
         for (int j = 0; j < TN; ++j) bf[buf][j] = *reinterpret_cast<const v4i *>(Bs + b_lane + j * 32 * ROW + kk);
+#pragma unroll
+        for (int i = 1; i < TM; ++i) af[buf][i] = *reinterpret_cast<const v4i *>(As + a_lane + i * 32 * ROW + kk);
     };
-    // Chunk q (0 .. A_CHUNKS+B_CHUNKS-1) of a stage: A rows for q < A_CHUNKS, else B rows.
+    // Chunk q (0 .. Q-1) of a stage: A rows for q < A_CHUNKS, else B rows.
     auto load_chunk = [&](v4u &dst, int q, int k0) {
         if (q < A_CHUNKS)
             dst = __builtin_amdgcn_raw_buffer_load_b128(ra, a_off + static_cast<uint32_t>(q * RPI) * lda + k0, 0, 0);
@@ -512,7 +512,6 @@ __global__ __launch_bounds__(kThreads) void w8a8_gemm_stream_kernel(GemmArgs arg
         *reinterpret_cast<v4u *>(stage + st_off + row0 * ROW) = src;
     };
 
-    constexpr int Q = A_CHUNKS + B_CHUNKS;
     v4u regs0[Q], regs1[Q];
     const int stages = args.k / BKT;
 #pragma unroll
@@ -543,24 +542,16 @@ __global__ __launch_bounds__(kThreads) void w8a8_gemm_stream_kernel(GemmArgs arg
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks & 1][i], bf[ks & 1][j], acc[i][j], 0, 0, 0);
-            // One memory instruction after each MFMA: reads, then writes, then loads.
+            // Issue order: after MFMA t, fragment read t (t < 6), LDS writes
+            // after MFMAs 2-3, global loads after MFMAs 5-6.
             constexpr int reads = (ks + 1 < KSTEPS) ? TM + TN : 0;
 #pragma unroll
-            for (int t = 0; t < reads; ++t) {
+            for (int t = 0; t < TM * TN; ++t) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                if (t < reads) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                if (t >= 2 && t < 2 + PER_STEP) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+                if (t >= 5 && t < 5 + PER_STEP) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
             }
-#pragma unroll
-            for (int t = 0; t < PER_STEP; ++t) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
-            }
-#pragma unroll
-            for (int t = 0; t < PER_STEP; ++t) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - reads - 2 * PER_STEP, 0);
             __builtin_amdgcn_sched_barrier(0);
         };
         kstep(std::integral_constant<int, 0>{});
@@ -578,8 +569,11 @@ __global__ __launch_bounds__(kThreads) void w8a8_gemm_stream_kernel(GemmArgs arg
     }
     if (s < stages) stage_body(s, regs0, regs1);
 
+    // Epilogue: LDS free once every wave is past its last fragment read.
     __syncthreads();
-    epilogue_256<EPI>(args, acc, m0, n0, wm, wn, lane, smem);
+    float *scales = reinterpret_cast<float *>(smem + 128 * 1024);
+    stage_scales<BM, BN, EPI>(args, scales, m0, n0);
+    store_tile_rows<EPI>(args, acc, m0, n0, wm, wcol, lane, smem, scales);
 }
 
 // ----------------------------------------------------------------------------
@@ -847,7 +841,7 @@ int launch_stream(const GemmArgs &args, int epi, hipStream_t stream) {
     auto kernel = epi == EPI_I32        ? w8a8_gemm_stream_kernel<EPI_I32>
                   : epi == EPI_DEQUANT ? w8a8_gemm_stream_kernel<EPI_DEQUANT>
                                        : w8a8_gemm_stream_kernel<EPI_DEQUANT_BIAS>;
-    return launch("w8a8_gemm_kernel", kernel, grid, dim3(kThreads), 0, stream, a2);
+    return launch("w8a8_gemm_kernel", kernel, grid, dim3(big::THREADS), 0, stream, a2);
 }
 
 template <int MR, bool FUSED>
