@@ -604,9 +604,9 @@ __device__ __forceinline__ void store_one(const GemmArgs &args, int row, int col
 // fp32 activation rows quantised inside the GEMV workgroup (the dynamic
 // W8A8 linear at M <= 4): same rule as qxt_quantize_rows_int8, computed by
 // every workgroup; workgroup 0 also writes the int8 rows and scales to the
-// caller's workspaces (args.a / args.sa), as the two-kernel path does.
-// fp32 chunks of 16 bytes per thread that hold a whole quantised row: the
-// fused path runs for K <= 16384.
+// caller's workspaces (args.a / args.sa), as the two-kernel path does.  A
+// row is held in registers as RC 16-byte chunks per thread (RC = 4, 8, 16
+// for K <= 4096, 8192, 16384).
 constexpr int kGemvRowChunks = 16;
 
 struct FusedRows {
@@ -616,12 +616,27 @@ struct FusedRows {
     int floor;
 };
 
+// Load fp32 row r of the fused path into xv (zeros past K).
+template <int RC>
+__device__ __forceinline__ void load_row(const GemmArgs &args, const FusedRows &f, int r, v4u (&xv)[RC]) {
+    const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(f.x, f.x_bytes);
+    const int k4 = args.k / 4;
+    const uint32_t base = static_cast<uint32_t>(r) * f.ldx;
+#pragma unroll
+    for (int u = 0; u < RC; ++u) {
+        const int c = threadIdx.x + u * kThreads;
+        xv[u] = __builtin_amdgcn_raw_buffer_load_b128(rx, c < k4 ? base + c * 16 : kOutOfRange, 0, 0);
+    }
+}
+
 // Stage activation rows [0, MR) (zeros past M) as 16-byte chunks in LDS;
 // `row_sa` receives each row's scale (1 for stored int8 rows, whose scales
-// the epilogue reads from args.sa).
-template <int MR, bool FUSED>
+// the epilogue reads from args.sa).  Fused rows: row 0 arrives in `xv0`,
+// which the caller loaded (before its weight loads, so that waiting for the
+// row does not wait for them); later rows are loaded here.
+template <int MR, int RC, bool FUSED>
 __device__ __forceinline__ void stage_rows(const GemmArgs &args, const FusedRows &f, v4u *act, float *row_sa,
-                                           float *scratch) {
+                                           float *scratch, const v4u (&xv0)[RC]) {
     const int k16 = args.k / 16;
     if constexpr (!FUSED) {
         const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(args.a, args.a_bytes);
@@ -633,7 +648,6 @@ __device__ __forceinline__ void stage_rows(const GemmArgs &args, const FusedRows
         if (threadIdx.x < MR)
             row_sa[threadIdx.x] = (args.sa != nullptr && threadIdx.x < args.m) ? args.sa[threadIdx.x] : 0.0f;
     } else {
-        const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(f.x, f.x_bytes);
         uint32_t *aw = reinterpret_cast<uint32_t *>(act);
         const int k4 = args.k / 4;
         for (int r = 0; r < MR; ++r) {
@@ -641,18 +655,17 @@ __device__ __forceinline__ void stage_rows(const GemmArgs &args, const FusedRows
                 for (int c = threadIdx.x; c < k4; c += kThreads) aw[r * k4 + c] = 0;
                 continue;
             }
-            const uint32_t base = static_cast<uint32_t>(r) * f.ldx;
-            // The row is read once into registers (K <= 16384 here: at most
-            // 16 x 16 bytes per thread), reduced, then quantised from them.
-            v4u xv[kGemvRowChunks];
+            // The row is read once into registers, reduced, then quantised from them.
+            v4u xv[RC];
+            if (r == 0) {
+#pragma unroll
+                for (int u = 0; u < RC; ++u) xv[u] = xv0[u];
+            } else {
+                load_row<RC>(args, f, r, xv);
+            }
             float amax = 0.0f;
 #pragma unroll
-            for (int u = 0; u < kGemvRowChunks; ++u) {
-                const int c = threadIdx.x + u * kThreads;
-                xv[u] = __builtin_amdgcn_raw_buffer_load_b128(rx, c < k4 ? base + c * 16 : kOutOfRange, 0, 0);
-            }
-#pragma unroll
-            for (int u = 0; u < kGemvRowChunks; ++u)
+            for (int u = 0; u < RC; ++u)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fabsf(__uint_as_float(xv[u][e])));
 #pragma unroll
@@ -663,7 +676,7 @@ __device__ __forceinline__ void stage_rows(const GemmArgs &args, const FusedRows
             __syncthreads();  // scratch is reused by the next row
             const float sc = row_scale(amax, f.floor != 0);
 #pragma unroll
-            for (int u = 0; u < kGemvRowChunks; ++u) {
+            for (int u = 0; u < RC; ++u) {
                 const int c = threadIdx.x + u * kThreads;
                 if (c >= k4) break;
                 const v4u v = xv[u];
@@ -685,10 +698,10 @@ __device__ __forceinline__ void stage_rows(const GemmArgs &args, const FusedRows
 // Weight [N, K] (K contiguous): each wave owns 4 output columns and streams
 // their K bytes 1 KB per load instruction (lane l takes bytes 16 l .. 16 l + 15
 // of each kilobyte), four kilobytes ahead of the one being reduced, the
-// first four requested before the activation is staged.  A wave sum per
-// column ends it.
+// first four requested before the activation is staged (after the first
+// fused fp32 row).  A wave sum per column ends it.
 constexpr int kGemvColsNK = 16;  // per workgroup: 4 waves x 4 columns
-template <int MR, int EPI, bool FUSED>
+template <int MR, int RC, int EPI, bool FUSED>
 __global__ __launch_bounds__(kThreads) void w8a8_gemv_nk_kernel(GemmArgs args, FusedRows f) {
     extern __shared__ v4u act[];  // [MR][K / 16]
     __shared__ float row_sa[4];
@@ -709,10 +722,12 @@ __global__ __launch_bounds__(kThreads) void w8a8_gemv_nk_kernel(GemmArgs args, F
     // Four kilobytes of every column in flight: ring slot d holds chunk
     // c0 + 64 d of the current group of 256 chunks.
     constexpr int kDepth = 4;
+    v4u xv0[RC];
+    if constexpr (FUSED) load_row<RC>(args, f, 0, xv0);
     v4u ring[kDepth][4];
 #pragma unroll
     for (int d = 0; d < kDepth; ++d) load_cols(ring[d], lane + 64 * d);
-    stage_rows<MR, FUSED>(args, f, act, row_sa, scratch);
+    stage_rows<MR, RC, FUSED>(args, f, act, row_sa, scratch, xv0);
     int acc[4][MR];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -757,13 +772,15 @@ __global__ __launch_bounds__(kThreads) void w8a8_gemv_nk_kernel(GemmArgs args, F
 // wave owns column n0 + l; the four waves split K and add their exact
 // partial sums through LDS.
 constexpr int kGemvColsK4N = 64;
-template <int MR, int EPI, bool FUSED>
+template <int MR, int RC, int EPI, bool FUSED>
 __global__ __launch_bounds__(kThreads) void w8a8_gemv_k4n_kernel(GemmArgs args, FusedRows f) {
     extern __shared__ v4u act[];  // [MR][K / 16]
     __shared__ int part[4][MR][64];
     __shared__ float row_sa[4];
     __shared__ float scratch[kThreads / 64];
-    stage_rows<MR, FUSED>(args, f, act, row_sa, scratch);
+    v4u xv0[RC];
+    if constexpr (FUSED) load_row<RC>(args, f, 0, xv0);
+    stage_rows<MR, RC, FUSED>(args, f, act, row_sa, scratch, xv0);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = blockIdx.x * kGemvColsK4N + lane;
     const int k4 = args.k / 4;
@@ -844,24 +861,37 @@ int launch_stream(const GemmArgs &args, int epi, hipStream_t stream) {
     return launch("w8a8_gemm_kernel", kernel, grid, dim3(big::THREADS), 0, stream, a2);
 }
 
-template <int MR, bool FUSED>
-int launch_gemv(GemmArgs args, const FusedRows &f, int epi, uint32_t layout, hipStream_t stream) {
+template <int MR, int RC, bool FUSED>
+int launch_gemv_rc(GemmArgs args, const FusedRows &f, int epi, uint32_t layout, hipStream_t stream) {
     args.a_bytes = static_cast<uint32_t>(static_cast<size_t>(args.m - 1) * args.lda + args.k);
     const size_t lds = static_cast<size_t>(MR) * args.k;
     if (layout == QXT_W8A8_WEIGHT_K4N) {
         args.w_bytes = static_cast<uint32_t>(static_cast<size_t>(args.k / 4 - 1) * args.ldw + args.n * 4);
-        auto kernel = epi == EPI_I32        ? w8a8_gemv_k4n_kernel<MR, EPI_I32, FUSED>
-                      : epi == EPI_DEQUANT ? w8a8_gemv_k4n_kernel<MR, EPI_DEQUANT, FUSED>
-                                           : w8a8_gemv_k4n_kernel<MR, EPI_DEQUANT_BIAS, FUSED>;
+        auto kernel = epi == EPI_I32        ? w8a8_gemv_k4n_kernel<MR, RC, EPI_I32, FUSED>
+                      : epi == EPI_DEQUANT ? w8a8_gemv_k4n_kernel<MR, RC, EPI_DEQUANT, FUSED>
+                                           : w8a8_gemv_k4n_kernel<MR, RC, EPI_DEQUANT_BIAS, FUSED>;
         return launch("w8a8_gemv_kernel", kernel, dim3((args.n + kGemvColsK4N - 1) / kGemvColsK4N), dim3(kThreads), lds,
                       stream, args, f);
     }
     args.w_bytes = static_cast<uint32_t>(static_cast<size_t>(args.n - 1) * args.ldw + args.k);
-    auto kernel = epi == EPI_I32        ? w8a8_gemv_nk_kernel<MR, EPI_I32, FUSED>
-                  : epi == EPI_DEQUANT ? w8a8_gemv_nk_kernel<MR, EPI_DEQUANT, FUSED>
-                                       : w8a8_gemv_nk_kernel<MR, EPI_DEQUANT_BIAS, FUSED>;
+    auto kernel = epi == EPI_I32        ? w8a8_gemv_nk_kernel<MR, RC, EPI_I32, FUSED>
+                  : epi == EPI_DEQUANT ? w8a8_gemv_nk_kernel<MR, RC, EPI_DEQUANT, FUSED>
+                                       : w8a8_gemv_nk_kernel<MR, RC, EPI_DEQUANT_BIAS, FUSED>;
     return launch("w8a8_gemv_kernel", kernel, dim3((args.n + kGemvColsNK - 1) / kGemvColsNK), dim3(kThreads), lds,
                   stream, args, f);
+}
+
+// Fused rows are held as K / 1024 chunks per thread, rounded up to 4, 8 or 16
+// (fewer registers for short rows, more workgroups per CU).
+template <int MR, bool FUSED>
+int launch_gemv(const GemmArgs &args, const FusedRows &f, int epi, uint32_t layout, hipStream_t stream) {
+    if constexpr (FUSED) {
+        if (args.k <= 4 * 4 * kThreads) return launch_gemv_rc<MR, 4, true>(args, f, epi, layout, stream);
+        if (args.k <= 8 * 4 * kThreads) return launch_gemv_rc<MR, 8, true>(args, f, epi, layout, stream);
+        return launch_gemv_rc<MR, kGemvRowChunks, true>(args, f, epi, layout, stream);
+    } else {
+        return launch_gemv_rc<MR, 1, false>(args, f, epi, layout, stream);
+    }
 }
 
 template <bool FUSED>
