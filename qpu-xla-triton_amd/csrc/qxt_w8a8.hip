@@ -10,10 +10,12 @@
 // Built with -ffp-contract=off so the two multiplies and the add round
 // separately, which makes the result bit-identical to the NumPy oracle.
 //
-// Tiling: a 256-thread workgroup (4 waves, 2 x 2) owns a BM x BN output tile;
-// each wave owns a (BM/2) x (BN/2) sub-tile of 32 x 32 MFMA blocks.  K advances
-// in steps of 64 bytes; A and B tiles live in LDS with K contiguous per row,
-// padded to 80 bytes so the 16-byte fragment reads are bank-conflict free.
+// Tiling (w8a8_gemm_kernel): a 256-thread workgroup (4 waves, 2 x 2) owns a
+// BM x BN output tile; each wave owns a (BM/2) x (BN/2) sub-tile of 32 x 32
+// MFMA blocks.  K advances BKT bytes per stage; A and B tiles live in LDS
+// with K contiguous per row, padded by 16 bytes so the 16-byte fragment reads
+// are bank-conflict free.  The large-tile streaming kernel
+// (w8a8_gemm_stream_kernel) uses eight waves of 128 x 64 instead.
 // The MFMA lane layout: lane l supplies A[l % 32][k-chunk(l / 32)] and
 // B[k-chunk(l / 32)][l % 32] (the same 16 k values for both operands, so the
 // exact integer sum does not depend on how the chunk is ordered) and receives
