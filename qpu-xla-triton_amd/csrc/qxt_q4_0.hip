@@ -56,7 +56,8 @@ namespace qxt {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr size_t kMaxLds = 64 * 1024;
+constexpr size_t kMaxLds = 64 * 1024;       // LDS a workgroup may use to stage its activation rows
+constexpr size_t kMaxLdsWide = 160 * 1024;  // gfx950 LDS per workgroup: wide single-linear tiles
 
 struct Q4Task {
     const float *x;        // fp32 rows quantised to Q8_0 in the workgroup, or nullptr
@@ -427,7 +428,22 @@ __global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Task t) {
     stage_activation<MR>(t, r0, aq, ad, geo);
     __syncthreads();
 
-    if constexpr (FAST) {
+    if constexpr (FAST && MR == 4 && !DOTS) {
+        // Wide tiles (several rounds of units): the next round's weights are
+        // requested before the current round is computed.
+        for (int first = 0; first < units; first += U * kThreads) {
+            uint32_t wn[U][36];
+            const bool more = first + U * kThreads < units;
+            if (more) load_units<U>(t, col_base, G, units, first + U * kThreads, wn);
+            compute_fast<MR, U, DOTS>(t, col_base, r0, G, units, first, wr, aq, ad, cb, geo);
+            if (more) {
+#pragma unroll
+                for (int j = 0; j < U; ++j)
+#pragma unroll
+                    for (int w = 0; w < 36; ++w) wr[j][w] = wn[j][w];
+            }
+        }
+    } else if constexpr (FAST) {
         for (int first = 0; first < units; first += U * kThreads) {
             if (first > 0) load_units<U>(t, col_base, G, units, first, wr);
             compute_fast<MR, U, DOTS>(t, col_base, r0, G, units, first, wr, aq, ad, cb, geo);
@@ -507,18 +523,23 @@ size_t lanes_bytes(uint64_t columns, uint64_t blocks) {
 }
 
 // Columns per workgroup (at most `max_cpw`) and dynamic LDS bytes for a task,
-// or an error status.
-int plan_task(Q4Task &t, int mr, bool fast, bool dots, size_t *lds, int max_cpw = 1 << 30) {
+// or an error status.  Normally a workgroup takes one round of units (a
+// unit per thread, U per thread on the fast path); `wide` takes max_cpw
+// columns, several rounds, within the whole LDS of a workgroup.
+int plan_task(Q4Task &t, int mr, bool fast, bool dots, size_t *lds, int max_cpw = 1 << 30, bool wide = false) {
     const Q4Lds geo(t.blocks, fast);
     const int units_per_col = fast ? t.blocks / 8 : t.blocks;
     const int per_round = kThreads * (fast ? units_per_thread(mr) : 1);
     int cpw = units_per_col >= per_round ? 1 : per_round / units_per_col;
+    if (wide) cpw = max_cpw;
     cpw = std::max(1, std::min({cpw, t.ncols, max_cpw}));
-    while (cpw > 1 && geo.words(mr, dots ? 0 : cpw) * 4 > kMaxLds) --cpw;
-    *lds = geo.words(mr, dots ? 0 : cpw) * 4;
-    if (*lds > kMaxLds)
-        return fail(QXT_CAPABILITY_MISSING, "q4_0 linear: K=%d needs %zu bytes of LDS (> %zu)", t.blocks * 32, *lds,
+    const size_t cap = wide ? kMaxLdsWide : kMaxLds;
+    while (cpw > 1 && geo.words(mr, dots ? 0 : cpw) * 4 > cap) --cpw;
+    const size_t narrow = geo.words(mr, dots ? 0 : 1) * 4;
+    if (narrow > kMaxLds)
+        return fail(QXT_CAPABILITY_MISSING, "q4_0 linear: K=%d needs %zu bytes of LDS (> %zu)", t.blocks * 32, narrow,
                     kMaxLds);
+    *lds = geo.words(mr, dots ? 0 : cpw) * 4;
     t.cpw = cpw;
     return QXT_OK;
 }
@@ -527,12 +548,18 @@ template <int MR, bool DOTS>
 int launch_single(Q4Task t, hipStream_t stream) {
     const bool fast = fast_path(t);
     // A single linear is latency-bound unless its grid covers the chip: cap
-    // the tile width so that there are at least two workgroups per CU.
+    // the tile width so that there are at least two workgroups per CU.  Four
+    // rows on the fast path instead give each CU one wide workgroup that
+    // streams its columns in rounds with the next round's weights in flight
+    // (measured on MI355X, cfg2: 14.8 -> 13.4 us at N = 11008 and 8.7 -> 7.6 us
+    // at N = 4096, K = 4096; the narrow tiles' LDS held N = 11008 to two
+    // workgroups per CU, 1.34 rounds).
     const int row_groups = (t.rows + MR - 1) / MR;
-    const long want = 2L * compute_units();
+    const bool wide = MR == 4 && fast && !DOTS;
+    const long want = (wide ? 1L : 2L) * compute_units();
     const int max_cpw = static_cast<int>(std::max<long>(1, (static_cast<long>(t.ncols) * row_groups + want - 1) / want));
     size_t lds = 0;
-    int rc = plan_task(t, MR, fast, DOTS, &lds, max_cpw);
+    int rc = plan_task(t, MR, fast, DOTS, &lds, max_cpw, wide);
     if (rc != QXT_OK) return rc;
     dim3 grid((t.ncols + t.cpw - 1) / t.cpw, row_groups, 1);
     constexpr int U = units_per_thread(MR);
