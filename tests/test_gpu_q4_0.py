@@ -71,6 +71,8 @@ def test_reference_seed_fixture_bit_exact_and_block_dots() -> None:
         (5, 24, 40),     # row group 4 + 1
         (16, 8, 48),
         (1, 1024, 16),   # K=32768: 128 units per column, two columns per workgroup
+        (4, 128, 11000),  # four rows, wide tiles: 43 columns per workgroup in three rounds, ragged last tile
+        (8, 128, 4100),   # two row groups of wide tiles, three rounds per workgroup
     ],
 )
 def test_random_shapes_bit_exact(rows: int, blocks: int, outputs: int) -> None:
@@ -354,6 +356,7 @@ def test_lane_pack_kernel_matches_the_layout_definition(n: int, blocks: int) -> 
 @pytest.mark.parametrize("rows,k,n,wcol0,ncols", [
     (1, 2048, 5632, 0, 5632),   # cfg0
     (4, 4096, 4096, 0, 4096),   # cfg2 (K=4096, N=4096)
+    (4, 4096, 11000, 8, 10984),  # wide four-row tiles over lane weights, several rounds, ragged
     (1, 5632, 2048, 16, 2032),  # a column range starting inside a lane group
     (2, 256, 37, 5, 31),        # a partial last group, any column range
     (17, 512, 64, 0, 64),       # rows beyond one MFMA-free row group
