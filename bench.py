@@ -183,6 +183,73 @@ def _rs(t) -> int:
     return int(t.stride(0)) * t.element_size()
 
 
+# ------------------------------------------------------------ output checks
+# After its timed region, every leg checks outputs of the launches it timed
+# against a torch restatement of the reference arithmetic on the host: exact
+# integer dots and the same fp32 roundings in the same order, so the check is
+# bit-exact.  (The NumPy oracle is test infrastructure; only the CPU-baseline
+# legs run it.)  A mismatch stops the run.
+
+
+def _fp16_field(torch, blocks):
+    return blocks[..., 0:2].contiguous().view(torch.float16)[..., 0].float()
+
+
+def check_q4_0(torch, label: str, q8_blocks, q4_blocks, output, rows=(0,)) -> dict:
+    """output[r, :N] == sum_b fl32(fl32(float(dot_b) * dw) * da) in block order, for r in rows."""
+    w = q4_blocks.cpu()
+    dw = _fp16_field(torch, w)  # [N, B]
+    codes = w[..., 2:].to(torch.int32)
+    qw = torch.cat([(codes & 15) - 8, (codes >> 4) - 8], dim=-1)  # [N, B, 32]
+    for r in rows:
+        a = q8_blocks[r].cpu()
+        da = _fp16_field(torch, a)  # [B]
+        qa = a[..., 2:].view(torch.int8).to(torch.int32)  # [B, 32]
+        dots = (qw * qa).sum(-1)  # [N, B], exact
+        acc = torch.zeros(w.shape[0], dtype=torch.float32)
+        for b in range(w.shape[1]):
+            acc = acc + (dots[:, b].float() * dw[:, b]) * da[b]
+        got = output[r, : w.shape[0]].cpu()
+        if not torch.equal(got, acc):
+            bad = int((got != acc).sum())
+            raise RuntimeError(f"{label}: row {r}: {bad} of {acc.numel()} outputs differ from the reference arithmetic")
+    return {"rows_checked": list(rows), "columns": int(w.shape[0]), "bit_exact": True}
+
+
+def check_w8a8(torch, label: str, x, qa, sa, weight, bias, y, rows=(0,)) -> dict:
+    """Row quantiser (scale floor 1/127, rint of the true quotient) and acc*sa*sw + bias, bit for bit."""
+    values = weight.values.cpu().to(torch.int64)
+    sw = weight.scales.cpu()
+    b = None if bias is None else bias.cpu()
+    floor = torch.tensor(1.0 / 127.0, dtype=torch.float32)
+    for r in rows:
+        xr = x[r].cpu()
+        scale = torch.maximum(xr.abs().max() / 127.0, floor)
+        q = torch.clamp(torch.round(xr / scale), -127, 127).to(torch.int8)
+        if not torch.equal(qa[r, : xr.numel()].cpu(), q) or not torch.equal(sa[r].cpu(), scale):
+            raise RuntimeError(f"{label}: row {r}: quantised activation differs from the reference rule")
+        acc = (values @ q.to(torch.int64)).to(torch.float32)
+        want = (acc * scale) * sw
+        if b is not None:
+            want = want + b
+        if not torch.equal(y[r].cpu(), want):
+            bad = int((y[r].cpu() != want).sum())
+            raise RuntimeError(f"{label}: row {r}: {bad} of {want.numel()} outputs differ from the reference arithmetic")
+    return {"rows_checked": list(rows), "columns": int(sw.numel()), "bit_exact": True}
+
+
+def q8_0_host(torch, values):
+    """fp32 rows [R, K] -> Q8_0 blocks [R, K/32, 34] on the host: d = absmax/127, q = clamp(rint(x * (1/d)))."""
+    v = values.cpu().reshape(values.shape[0], -1, 32)
+    d = v.abs().amax(dim=2) / 127.0
+    inv = torch.where(d != 0, 1.0 / d, torch.zeros_like(d))
+    q = torch.clamp(torch.round(v * inv[..., None]), -127, 127).to(torch.int8)
+    out = torch.empty((v.shape[0], v.shape[1], 34), dtype=torch.uint8)
+    out[..., 0:2] = d.half().view(torch.uint8).reshape(v.shape[0], v.shape[1], 2)
+    out[..., 2:] = q.view(torch.uint8)
+    return out
+
+
 # --------------------------------------------------------------------- legs
 
 
@@ -306,6 +373,12 @@ def leg_decode(torch, args) -> dict:
         "prepass_avg_us": float(np.mean(prepass)) * 1e3,
         "prepass_bytes_per_launch": prepass_bytes,
     }
+    torch.cuda.synchronize()
+    result["batched"]["check"] = {
+        f"linear_{i}": check_q4_0(torch, f"decode batched linear {i}", q8_0_host(torch, linears[i]["x"]),
+                                  linears[i]["weight"], linears[i]["y"])
+        for i in (0, len(linears) // 2, len(linears) - 1)
+    }
     log(f"decode batched: {result['batched']}")
 
     # staged: one batch per dependency stage.
@@ -330,6 +403,9 @@ def leg_decode(torch, args) -> dict:
         "kernel_sum_us_per_step": float(np.sum(stimes)) * 1e3 / 2,
     }
     del graph
+    torch.cuda.synchronize()
+    last = linears[-1]
+    result["staged"]["check"] = check_q4_0(torch, "decode staged", q8_0_host(torch, last["x"]), last["weight"], last["y"])
     log(f"decode staged: {result['staged']}")
 
     # per_linear: quantise kernel + GEMV kernel per linear.
@@ -355,6 +431,9 @@ def leg_decode(torch, args) -> dict:
         "q8_0_avg_us": float(np.mean(ptimes.get("q8_0_kernel", [0.0]))) * 1e3,
     }
     del graph
+    torch.cuda.synchronize()
+    result["per_linear"]["check"] = check_q4_0(torch, "decode per_linear", q8_0_host(torch, last["x"]),
+                                               last["weight"], last["y"])
     log(f"decode per_linear: {result['per_linear']}")
     batch.close()
     for st in stages:
@@ -379,7 +458,8 @@ def leg_rotated_q4(torch, args, rows: int, k: int, n: int, seed: int) -> dict:
     weights = []
     for _ in range(copies):
         w = torch.randn((n, k), generator=gen, device="cuda", dtype=torch.float32) * 0.02
-        weights.append(pack_ggml_q4_0_lane_weights(quantize_q4_0(w)))
+        last_native = quantize_q4_0(w)  # kept for the output check of the last launch
+        weights.append(pack_ggml_q4_0_lane_weights(last_native))
         del w
     x = torch.randn((rows, k), generator=gen, device="cuda", dtype=torch.float32)
     xq = quantize_q8_0(x)
@@ -406,10 +486,17 @@ def leg_rotated_q4(torch, args, rows: int, k: int, n: int, seed: int) -> dict:
         "stream_us_per_launch": wall_ms * 1e3 / copies,
         "stream_gbs": b * copies / (wall_ms * 1e-3) / 1e9,
     }
-    del graph, weights
+    torch.cuda.synchronize()
+    out["check"] = check_q4_0(torch, out["shape"], q8_0_host(torch, x), last_native, y, rows=tuple(range(rows)))
+    del graph, weights, last_native
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     return out
+
+
+def gemm_kernel_ms(times: dict[str, list[float]]) -> float:
+    """Total device ms of the W8A8 GEMM launches (256 x 256 stream kernel and the tiled kernel)."""
+    return float(sum(np.sum(v) for name, v in times.items() if name.startswith("w8a8_gemm")))
 
 
 def _w8a8_operands(torch, gen, m: int, k: int, n: int):
@@ -458,7 +545,7 @@ def leg_w8a8(torch, args, shapes: dict | None = None) -> dict:
         wall_ms = modes[mode]
         ops = 2 * m * n * k
         # Per operator call (a GEMM may be two launches: full tiles + a half-tile round).
-        gemm_ms = float(np.sum(times["w8a8_gemm_kernel"])) / reps
+        gemm_ms = gemm_kernel_ms(times) / reps
         quant_ms = float(np.sum(times["rows_int8_kernel"])) / reps
         result[label] = {
             "shape": f"M={m} K={k} N={n}",
@@ -471,6 +558,8 @@ def leg_w8a8(torch, args, shapes: dict | None = None) -> dict:
             "gemm_frac_mfma": ops / (gemm_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS,
             "row_quantise_ms": quant_ms,
         }
+        torch.cuda.synchronize()
+        result[label]["check"] = check_w8a8(torch, f"w8a8 {label}", x, qa, sa, weight, bias, y, rows=(0, m - 1))
         total_ops += ops
         total_ms += wall_ms
         total_gemm_ms += gemm_ms
@@ -482,10 +571,10 @@ def leg_w8a8(torch, args, shapes: dict | None = None) -> dict:
     result["unit"] = "TOPS"
     result["roofline"] = {
         "bound": "mfma",
-        "kernel": "w8a8_gemm_kernel",
+        "kernel": "w8a8_gemm_stream_kernel",
         "achieved": gemm_tops,
         "peak": PEAK_INT8_TOPS,
-        "unit": "TFLOP/s",
+        "unit": "TOPS",
         "frac": gemm_tops / PEAK_INT8_TOPS,
         "ops_per_launch": total_ops // 2,
     }
@@ -549,6 +638,8 @@ def leg_w8a8_gemv(torch, args) -> dict:
             # M <= 4 quantises inside the GEMV kernel: one launch per operator call.
             "launches_per_call": sum(len(v) for v in times.values()) // (2 * copies),
         }
+        torch.cuda.synchronize()
+        out[label]["check"] = check_w8a8(torch, f"w8a8 gemv {label}", x, qa, sa, weights[-1], bias, y)
         del graph, weights
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
@@ -577,7 +668,8 @@ def leg_prefill(torch, args) -> dict:
     out = {}
     for label, (k, n) in {"gate_up": (2048, 5632), "down": (5632, 2048)}.items():
         wq = quantize_q4_0(torch.randn((n, k), generator=gen, device="cuda") * 0.02)
-        xq = quantize_q8_0(torch.randn((rows, k), generator=gen, device="cuda"))
+        x = torch.randn((rows, k), generator=gen, device="cuda")
+        xq = quantize_q8_0(x)
         w_scales, w_words = pack_ggml_q4_0_tiled_weights(wq)
         a_scales, a_values = split_ggml_q8_0_blocks(xq)
         y = torch.empty((rows, n), dtype=torch.float32, device="cuda")
@@ -606,8 +698,10 @@ def leg_prefill(torch, args) -> dict:
             "tops": 2 * rows * n * k / (best * 1e-6) / 1e12,
             "valu_bound_us": valu_ops / valu_peak * 1e6,
             "frac_valu_bound": valu_ops / valu_peak / (best * 1e-6),
+            "check": check_q4_0(torch, f"prefill {label}", q8_0_host(torch, x[[0, rows - 1]]), wq,
+                                y[[0, rows - 1]], rows=(0, 1)),
         }
-        del wq, xq, y, y_split, w_scales, w_words, a_scales, a_values
+        del wq, x, xq, y, y_split, w_scales, w_words, a_scales, a_values
         torch.cuda.synchronize()
     return out
 
@@ -652,6 +746,15 @@ def leg_geglu(torch, args) -> dict:
             "gbs": nbytes / (us * 1e-6) / 1e9,
             "frac_hbm_peak": nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS,
         }
+        # Last launch: v = fl32(table[fp16(gate)] * up), then the Q8_0 rule, on row 0.
+        torch.cuda.synchronize()
+        gate, up, q8 = sets[-1]
+        index = gate[0].cpu().half().view(torch.int16).to(torch.int64) & 0xFFFF
+        gelu = table.cpu().view(torch.int16)[index].view(torch.float16).float()
+        want = q8_0_host(torch, (gelu * up[0].cpu())[None])
+        if not torch.equal(q8[0].cpu(), want[0]):
+            raise RuntimeError(f"geglu M={rows}: row 0 differs from the reference arithmetic")
+        out[f"m{rows}"]["check"] = {"rows_checked": [0], "blocks": k // 32, "bit_exact": True}
         del sets
         torch.cuda.empty_cache()
     return out
@@ -678,10 +781,13 @@ def leg_cfg1(torch, args) -> dict:
     times = runner.kernel_times()
     graph = runner.capture()
     wall_ms, _ = runner.timed_graph(graph, 10, 2)
+    torch.cuda.synchronize()
+    check = check_w8a8(torch, "cfg1", x, qa, sa, weight, bias, y, rows=(0, m - 1))
     return {
+        "check": check,
         "shape": "M=K=N=512",
         "operator_us": wall_ms * 1e3 / 32,
-        "gemm_kernel_us": float(np.sum(times["w8a8_gemm_kernel"])) * 1e3 / 32,
+        "gemm_kernel_us": gemm_kernel_ms(times) * 1e3 / 32,
         "quantise_kernel_us": float(np.sum(times["rows_int8_kernel"])) * 1e3 / 32,
         "operator_tops": 2 * m * n * k / (wall_ms * 1e-3 / 32) / 1e12,
     }

@@ -24,8 +24,10 @@
  *  - the CPU_REPACK weight layout (block_q4_0x4, nibbles XOR 0x88) is accepted
  *    directly (weight_format) and unpacked on the GPU, instead of by the
  *    caller (integrations/llama_cpp/backend/ggml-qpu.cpp:250-284);
- *  - there is no qpu_llama_q4_0_submission_cpu_fallback: the library has no
- *    CPU compute path;
+ *  - qxt_llama_q4_0_submission_cpu_fallback exists (so a caller written for
+ *    the reference links and keeps its control flow) but computes nothing:
+ *    the library has no CPU compute path, so it returns
+ *    QXT_CAPABILITY_MISSING and leaves the destination untouched;
  *  - only QXT_LLAMA_Q4_0_WEIGHT_EXACT is provided; the reference's approximate
  *    COLUMN_W8 / ROWCOL_W8A8 modes return QXT_CAPABILITY_MISSING.
  */
@@ -122,6 +124,11 @@ void qxt_llama_context_destroy(qxt_llama_context *context);
 const char *qxt_llama_context_last_error(const qxt_llama_context *context);
 void qxt_llama_context_set_failure_mask(qxt_llama_context *context, uint32_t failure_mask);
 
+/* Text of a status ("ok", "invalid argument", ...); replaces
+ * qpu_llama_status_string (qpu_llama_runtime.h:133).  Same strings as
+ * qxt_status_string. */
+const char *qxt_llama_status_string(int status);
+
 /* Hash of the kernel sources this library was built from: the value
  * desc.expected_source_hash must carry (the reference's generated
  * *_source_hash strings, ggml-qpu.cpp:349). */
@@ -143,6 +150,14 @@ int qxt_llama_q4_0_submission_wait(qxt_llama_q4_0_submission *submission, qxt_ll
 void qxt_llama_q4_0_submission_destroy(qxt_llama_q4_0_submission *submission);
 int qxt_llama_q4_0_linear_execute(qxt_llama_q4_0_linear *linear, const qxt_llama_q4_0_execution *execution,
                                   qxt_llama_q4_0_timing *timing);
+
+/* Replaces qpu_llama_q4_0_submission_cpu_fallback (qpu_llama_q4_0.h:79-80),
+ * which the reference's M=1 hook calls after a failed wait
+ * (backend/ggml-qpu-up-inline.cpp:379-388).  This library has no CPU compute
+ * path: NULL -> QXT_INVALID_ARGUMENT; otherwise QXT_CAPABILITY_MISSING with
+ * the context's last error set and no byte of the destination written, so the
+ * caller's own CPU path computes the columns. */
+int qxt_llama_q4_0_submission_cpu_fallback(qxt_llama_q4_0_submission *submission);
 
 #ifdef __cplusplus
 }

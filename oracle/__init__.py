@@ -49,9 +49,16 @@ Pinning status (what each function is checked against, in ``tests/``):
   gelu is the identity or exactly zero); dequantised blocks within half a
   step of gelu(gate) * up computed in float64; the split planes against the
   native blocks byte for byte.
-* ``quantize_q4_0_blocks``: PARITY UNPINNED against upstream ggml
-  ``quantize_row_q4_0`` (ggml is not vendored in the reference); only the
-  BASELINE formula's invariants are checked.
+* ``quantize_q4_0_blocks``: ggml's published ``quantize_row_q4_0_ref`` rule
+  (upstream ggml is not vendored in the reference, so there is no runnable
+  copy); pinned by hand-worked known-answer blocks whose literal codes and
+  fp16 scale bits separate the plausible mistakes (half-way values round up,
+  not to even and not by truncating x/d + 8; the first element of largest
+  magnitude sets the sign; x * fl32(1/d), not x / d; codes from the fp32 d,
+  not its fp16 rounding; -0.0 scale of a zero block; fp16-subnormal scales),
+  by the same blocks and random blocks re-derived in exact rational
+  arithmetic with explicit round-to-fp32 steps, and by the half-step
+  reconstruction bound (``tests/test_oracle_ggml.py``).
 """
 
 from oracle.ggml import (  # noqa: F401

@@ -173,12 +173,14 @@ def quantize_q8_0_blocks(values: np.ndarray) -> np.ndarray:
 def quantize_q4_0_blocks(weights: np.ndarray) -> np.ndarray:
     """Quantise fp32 rows [N, K] into native Q4_0 blocks u8 [N, K/32, 18].
 
-    PARITY UNPINNED against upstream ggml: the reference has no Python Q4_0
-    quantiser and only calls ggml's ``quantize_row_q4_0`` from native tests
-    (``integrations/llama_cpp/tests/qpu_ggml_backend_smoke.cpp:119``; llama.cpp
-    pinned at 91d2fc387529940230555abd297a8b5e99737d3f, not vendored).  This
-    restates ggml's published reference quantiser, which implements the
-    BASELINE formula ``d = signed_absmax / -8``, ``q = clamp(round(x/d) + 8, 0, 15)``:
+    Restates ggml's published reference quantiser ``quantize_row_q4_0_ref``
+    (the reference has no Python Q4_0 quantiser and calls ggml's
+    ``quantize_row_q4_0`` only from native tests,
+    ``integrations/llama_cpp/tests/qpu_ggml_backend_smoke.cpp:119``; llama.cpp
+    pinned at 91d2fc387529940230555abd297a8b5e99737d3f, not vendored), the
+    BASELINE formula ``d = signed_absmax / -8``, ``q = clamp(round(x/d) + 8, 0, 15)``
+    with ggml's rounding.  Pinned by the known-answer blocks of
+    ``tests/q4_0_kats.py`` (literal codes) and by exact rational arithmetic:
 
     * ``max`` = the first element of largest magnitude (+0.0 for an all-zero block),
     * ``d = fl32(max / -8)``, ``id = fl32(1 / d)`` or 0 when d == 0,

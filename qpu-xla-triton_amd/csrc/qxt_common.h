@@ -63,6 +63,11 @@ int q4_0_tiled_native(const void *activation, size_t activation_row_stride, cons
                       uint32_t blocks, uint32_t weight_column_start, uint32_t output_column_start,
                       uint32_t column_count, hipStream_t stream);
 
+// QXT_OK when a Q4_0 linear of `rows` rows and `blocks` blocks fits the LDS of
+// one workgroup on the v_dot4 path, else QXT_CAPABILITY_MISSING with a
+// message (qxt_q4_0.hip).
+int q4_0_linear_capability(uint32_t rows, uint32_t blocks);
+
 // -------------------------------------------------------------- device side
 
 constexpr int QK = 32;            // elements per GGML block

@@ -326,6 +326,8 @@ extern "C" void qxt_llama_context_set_failure_mask(qxt_llama_context *context, u
 
 extern "C" const char *qxt_llama_q4_0_source_hash(void) { return QXT_Q4_0_SOURCE_HASH; }
 
+extern "C" const char *qxt_llama_status_string(int status) { return qxt_status_string(status); }
+
 // ------------------------------------------------------------------ linear
 
 extern "C" int qxt_llama_q4_0_linear_prepare(qxt_llama_context *context, const qxt_llama_q4_0_linear_desc *d,
@@ -357,6 +359,10 @@ extern "C" int qxt_llama_q4_0_linear_prepare(qxt_llama_context *context, const q
     }
     if (d->weight_mode != QXT_LLAMA_Q4_0_WEIGHT_EXACT)
         return context->fail(QXT_CAPABILITY_MISSING, "q4_0 prepare: only the exact weight mode is provided");
+    // Every submission (any row count up to d->rows) must be runnable: reject
+    // a K whose activation rows do not fit a workgroup's LDS now, not at submit.
+    if (qxt::q4_0_linear_capability(d->rows, static_cast<uint32_t>(blocks)) != QXT_OK)
+        return context->fail(QXT_CAPABILITY_MISSING, "q4_0 prepare: %s", qxt_last_error());
     if (context->injected(QXT_FAIL_SOURCE_HASH)) return context->fail(QXT_HASH_MISMATCH, "injected source hash mismatch");
     if (std::strcmp(d->expected_source_hash, QXT_Q4_0_SOURCE_HASH) != 0)
         return context->fail(QXT_HASH_MISMATCH, "expected source hash %.64s does not match this build (%s)",
@@ -590,4 +596,13 @@ extern "C" int qxt_llama_q4_0_linear_execute(qxt_llama_q4_0_linear *linear, cons
     if (rc == QXT_OK) rc = qxt_llama_q4_0_submission_wait(submission, timing);
     qxt_llama_q4_0_submission_destroy(submission);
     return rc;
+}
+
+// No CPU compute path: the reference's fallback recomputes the submission on
+// the host (qpu_llama_q4_0.c:834-946); here the caller's own CPU kernel does,
+// so the destination is left exactly as it was.
+extern "C" int qxt_llama_q4_0_submission_cpu_fallback(qxt_llama_q4_0_submission *submission) {
+    if (submission == nullptr || submission->linear == nullptr) return QXT_INVALID_ARGUMENT;
+    return submission->linear->context->fail(QXT_CAPABILITY_MISSING,
+                                             "q4_0 cpu fallback: this library has no CPU compute path");
 }

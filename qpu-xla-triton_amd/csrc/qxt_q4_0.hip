@@ -524,8 +524,11 @@ size_t lanes_bytes(uint64_t columns, uint64_t blocks) {
 
 // Columns per workgroup (at most `max_cpw`) and dynamic LDS bytes for a task,
 // or an error status.  Normally a workgroup takes one round of units (a
-// unit per thread, U per thread on the fast path); `wide` takes max_cpw
-// columns, several rounds, within the whole LDS of a workgroup.
+// unit per thread, U per thread on the fast path) within kMaxLds; `wide`
+// takes max_cpw columns, several rounds, within the whole LDS of a
+// workgroup.  A K whose single-column tile exceeds kMaxLds also runs, on
+// fewer workgroups per CU, up to the whole LDS (about K = 111k at one row,
+// 55k at two, 37k at three and 27k at four rows).
 int plan_task(Q4Task &t, int mr, bool fast, bool dots, size_t *lds, int max_cpw = 1 << 30, bool wide = false) {
     const Q4Lds geo(t.blocks, fast);
     const int units_per_col = fast ? t.blocks / 8 : t.blocks;
@@ -533,12 +536,12 @@ int plan_task(Q4Task &t, int mr, bool fast, bool dots, size_t *lds, int max_cpw 
     int cpw = units_per_col >= per_round ? 1 : per_round / units_per_col;
     if (wide) cpw = max_cpw;
     cpw = std::max(1, std::min({cpw, t.ncols, max_cpw}));
-    const size_t cap = wide ? kMaxLdsWide : kMaxLds;
-    while (cpw > 1 && geo.words(mr, dots ? 0 : cpw) * 4 > cap) --cpw;
     const size_t narrow = geo.words(mr, dots ? 0 : 1) * 4;
-    if (narrow > kMaxLds)
-        return fail(QXT_CAPABILITY_MISSING, "q4_0 linear: K=%d needs %zu bytes of LDS (> %zu)", t.blocks * 32, narrow,
-                    kMaxLds);
+    const size_t cap = (wide || narrow > kMaxLds) ? kMaxLdsWide : kMaxLds;
+    if (narrow > cap)
+        return fail(QXT_CAPABILITY_MISSING, "q4_0 linear: K=%d at %d rows needs %zu bytes of LDS (> %zu)",
+                    t.blocks * 32, mr, narrow, cap);
+    while (cpw > 1 && geo.words(mr, dots ? 0 : cpw) * 4 > cap) --cpw;
     *lds = geo.words(mr, dots ? 0 : cpw) * 4;
     t.cpw = cpw;
     return QXT_OK;
@@ -577,6 +580,22 @@ int dispatch_single(const Q4Task &t, hipStream_t stream) {
         default: return launch_single<4, DOTS>(t, stream);
     }
 }
+
+}  // namespace
+
+// Whether a single linear of `rows` rows and `blocks` blocks fits a workgroup's
+// LDS on the v_dot4 path (the path every row count below 16 takes, and larger
+// row counts when the matrix-core kernel does not apply).
+int q4_0_linear_capability(uint32_t rows, uint32_t blocks) {
+    Q4Task t{};
+    t.blocks = static_cast<int>(blocks);
+    t.ncols = 1;
+    const int mr = rows >= 4 ? 4 : static_cast<int>(rows);
+    size_t lds = 0;
+    return plan_task(t, mr, blocks % 8 == 0, false, &lds, 1, mr == 4 && blocks % 8 == 0);
+}
+
+namespace {
 
 int validate_q4(const void *activation, size_t activation_row_stride, const void *weight, size_t weight_row_stride,
                 uint32_t rows, uint32_t blocks, uint32_t column_count) {

@@ -865,7 +865,7 @@ int launch_stream(const GemmArgs &args, int epi, hipStream_t stream) {
     auto kernel = epi == EPI_I32        ? w8a8_gemm_stream_kernel<EPI_I32>
                   : epi == EPI_DEQUANT ? w8a8_gemm_stream_kernel<EPI_DEQUANT>
                                        : w8a8_gemm_stream_kernel<EPI_DEQUANT_BIAS>;
-    return launch("w8a8_gemm_kernel", kernel, grid, dim3(big::THREADS), 0, stream, a2);
+    return launch("w8a8_gemm_stream_kernel", kernel, grid, dim3(big::THREADS), 0, stream, a2);
 }
 
 template <int MR, int RC, bool FUSED>

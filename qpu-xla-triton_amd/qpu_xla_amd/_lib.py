@@ -1,5 +1,5 @@
-"""ctypes binding of ``libqxt_gfx950.so`` (declared in ``include/qxt_gfx950.h``
-and ``include/qxt_llama_q4_0.h``).
+"""ctypes binding of ``libqxt_gfx950.so`` (declared in ``include/qxt_gfx950.h``,
+``include/qxt_llama_q4_0.h`` and ``include/qxt_ggml_hooks.h``).
 
 The library is built in-tree by ``qpu-xla-triton_amd/build.py``.  There is no
 fallback: when the library is missing every entry point raises
@@ -190,6 +190,15 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "qxt_llama_q4_0_submission_wait": (c_int, [_P, POINTER(LlamaQ4_0Timing)]),
     "qxt_llama_q4_0_submission_destroy": (None, [_P]),
     "qxt_llama_q4_0_linear_execute": (c_int, [_P, POINTER(LlamaQ4_0Execution), POINTER(LlamaQ4_0Timing)]),
+    "qxt_llama_q4_0_submission_cpu_fallback": (c_int, [_P]),
+    "qxt_llama_status_string": (c_char_p, [c_int]),
+    # ggml CPU_REPACK M=1 hooks (include/qxt_ggml_hooks.h)
+    "ggml_qpu_m1_register_q4_0": (c_int, [c_char_p, _P, _SZ, c_uint64, c_uint64]),
+    "ggml_qpu_m1_weight_registered": (c_int, [c_char_p]),
+    "ggml_qpu_m1_execute": (c_int, [c_char_p, _P, _SZ, _P, c_uint64, c_uint64, c_uint64, c_uint64]),
+    "ggml_qpu_m1_cpu_columns_for": (c_uint64, [c_char_p]),
+    "ggml_qpu_m1_dispatch_count": (c_uint64, []),
+    "ggml_qpu_m1_release": (None, []),
 }
 
 

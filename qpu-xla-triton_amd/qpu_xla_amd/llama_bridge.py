@@ -29,6 +29,11 @@ def source_hash() -> str:
     return _lib.load().qxt_llama_q4_0_source_hash().decode()
 
 
+def status_string(status: int) -> str:
+    """``qxt_llama_status_string`` (the reference's ``qpu_llama_status_string`` texts)."""
+    return _lib.load().qxt_llama_status_string(status).decode()
+
+
 def _host_pointer(buffer: np.ndarray) -> int:
     if not isinstance(buffer, np.ndarray) or not buffer.flags["C_CONTIGUOUS"]:
         raise ValueError("bridge buffers must be C-contiguous NumPy arrays")
@@ -183,6 +188,10 @@ class Submission:
         timing = _lib.LlamaQ4_0Timing()
         status = _lib.load().qxt_llama_q4_0_submission_wait(self.handle, ctypes.byref(timing))
         return int(status), timing
+
+    def cpu_fallback_status(self) -> int:
+        """``qxt_llama_q4_0_submission_cpu_fallback``: always CAPABILITY_MISSING (no CPU compute path)."""
+        return int(_lib.load().qxt_llama_q4_0_submission_cpu_fallback(self.handle))
 
     def destroy(self) -> None:
         if self.handle:

@@ -265,6 +265,7 @@ class PreparedW8A8Linear:
         self._begin()
         self._bind(queue)
         self._check_io(destination, source)
+        queue.order_after_caller((destination, source))
         queue._wait_dependencies(wait_for)
         with torch.cuda.stream(queue.stream):
             src = self._staged(source)
@@ -287,6 +288,7 @@ class PreparedW8A8Linear:
             raise ValueError("prepared W8A8 linear destination shape does not align")
         if destination.device != self.device:
             raise DependencyError("prepared W8A8 linear destination must live on the plan device")
+        queue.order_after_caller((destination,))
         queue._wait_dependencies(wait_for)
         with torch.cuda.stream(queue.stream):
             w8a8_gemm_dequantize(
@@ -317,6 +319,8 @@ class PreparedW8A8Linear:
         if qpu_outputs <= 0 or qpu_outputs >= self.outputs or qpu_outputs % PARTITION_ALIGNMENT:
             raise ValueError("hybrid W8A8 qpu_outputs must be aligned and leave a non-empty tail")
         self._bind(qpu_queue, cpu_queue)
+        qpu_queue.order_after_caller((destination, source))
+        cpu_queue.order_after_caller((destination, source))
         qpu_queue._wait_dependencies(wait_for)
         cpu_queue._wait_dependencies(wait_for)
         split = int(qpu_outputs)
@@ -362,6 +366,8 @@ class PreparedW8A8Linear:
         if qpu_rows <= 0 or qpu_rows >= batch or qpu_rows % PARTITION_ALIGNMENT:
             raise ValueError("hybrid W8A8 qpu_rows must be aligned and leave a non-empty tail")
         self._bind(qpu_queue, cpu_queue)
+        qpu_queue.order_after_caller((destination, source))
+        cpu_queue.order_after_caller((destination, source))
         qpu_queue._wait_dependencies(wait_for)
         cpu_queue._wait_dependencies(wait_for)
         split = int(qpu_rows)

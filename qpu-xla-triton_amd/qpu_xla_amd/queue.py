@@ -7,6 +7,14 @@ worker, so this ``Queue`` enqueues each kernel on its HIP stream (through the
 C ABI, no thread hop) and records a HIP event after it.  ``wait_for`` events
 from other queues become stream waits.  ``host_task`` runs its callable on
 the calling thread once its dependencies have completed.
+
+Tensors cross from the caller's stream to the queue's the way torch expects
+of a side stream: every submission first makes the queue's stream wait for
+the caller's current stream (so an argument still being written there by
+asynchronous work is complete before the queue reads it), and every tensor
+argument is marked as used on the queue's stream (``record_stream``), so the
+caching allocator does not hand its memory out again while the queue's work
+on it is pending -- the caller may drop its references right after submit.
 """
 
 from __future__ import annotations
@@ -79,6 +87,21 @@ class Queue:
         """The raw ``hipStream_t`` of this queue."""
         return int(self.stream.cuda_stream)
 
+    def order_after_caller(self, tensors: Iterable[Any] = ()) -> None:
+        """Order this queue after the caller's current stream; keep ``tensors`` alive for it.
+
+        Called by every submission (and by the plans that launch on a queue):
+        the queue's stream waits for the work already issued on the caller's
+        current stream of this device, and each CUDA tensor in ``tensors`` is
+        recorded as used by the queue's stream.
+        """
+        current = torch.cuda.current_stream(self.device)
+        if current.cuda_stream != self.stream.cuda_stream:
+            self.stream.wait_stream(current)
+        for tensor in tensors:
+            if isinstance(tensor, torch.Tensor) and tensor.is_cuda:
+                tensor.record_stream(self.stream)
+
     def _wait_dependencies(self, wait_for: Iterable[Event]) -> None:
         for event in wait_for:
             if not isinstance(event, Event):
@@ -104,6 +127,7 @@ class Queue:
         if self._closed:
             raise DependencyError("queue is closed")
         launch = LaunchConfig(tuple(int(g) for g in grid))  # type: ignore[arg-type]
+        self.order_after_caller(args)
         self._wait_dependencies(wait_for)
         with torch.cuda.device(self.device):
             kernel.execute(self.handle, args, launch)

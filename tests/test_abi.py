@@ -10,6 +10,7 @@ import ctypes
 import re
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 from qpu_xla_amd import _lib
@@ -21,7 +22,9 @@ def declared_functions() -> list[str]:
     names: set[str] = set()
     for header in HEADERS:
         text = header.read_text()
-        names.update(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(qxt_\w+)\s*\(", text, flags=re.MULTILINE))
+        names.update(
+            re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*((?:qxt|ggml_qpu)_\w+)\s*\(", text, flags=re.MULTILINE)
+        )
     return sorted(names)
 
 
@@ -168,3 +171,54 @@ def test_llama_bridge_validates_on_the_host() -> None:
     lib.qxt_llama_q4_0_linear_destroy(None)
     lib.qxt_llama_q4_0_submission_destroy(None)
     lib.qxt_llama_context_destroy(None)
+
+
+def test_llama_status_string_matches_the_reference_texts() -> None:
+    from qpu_xla_amd.llama_bridge import status_string
+
+    # qpu_llama_runtime.c:751-765.
+    texts = ["ok", "invalid argument", "device unavailable", "capability missing", "allocation failed",
+             "I/O failed", "submission failed", "timeout", "hash mismatch", "internal error"]
+    for status, text in enumerate(texts):
+        assert status_string(status) == text
+    assert status_string(42) == "unknown status"
+
+
+def test_cpu_fallback_of_no_submission_is_invalid() -> None:
+    assert _lib.load().qxt_llama_q4_0_submission_cpu_fallback(None) == _lib.INVALID_ARGUMENT
+
+
+def test_ggml_m1_hooks_decline_without_opt_in(monkeypatch) -> None:
+    # Disabled or unselected tensors are declined before any HIP call.
+    from qpu_xla_amd import ggml_hooks
+
+    weights = np.zeros((16, 1, 18), np.uint8)
+    monkeypatch.delenv("GGML_QPU_M1_INLINE", raising=False)
+    monkeypatch.setenv("GGML_QPU_M1_TENSORS", "ffn_up")
+    assert not ggml_hooks.register_q4_0("blk.0.ffn_up.weight", weights, 32, 16)
+    monkeypatch.setenv("GGML_QPU_M1_INLINE", "1")
+    assert not ggml_hooks.register_q4_0("blk.0.attn_q.weight", weights, 32, 16)  # not selected
+    monkeypatch.setenv("GGML_QPU_M1_TENSORS", "")
+    assert not ggml_hooks.register_q4_0("blk.0.ffn_up.weight", weights, 32, 16)  # empty selection
+    monkeypatch.setenv("GGML_QPU_M1_TENSORS", "attn,ffn_up")
+    assert not ggml_hooks.register_q4_0("blk.0.ffn_up.weight", weights, 40, 16)  # K % 32
+    assert not ggml_hooks.register_q4_0("blk.0.ffn_up.weight", weights, 32, 24)  # N % 16
+    assert not ggml_hooks.weight_registered("blk.0.ffn_up.weight")
+    destination = np.zeros(16, np.float32)
+    activation = np.zeros((1, 34), np.uint8)
+    assert not ggml_hooks.execute("blk.0.ffn_up.weight", activation, destination, 32, 16)
+    assert ggml_hooks.cpu_columns_for("blk.0.ffn_up.weight") == 0
+    assert ggml_hooks.dispatch_count() == 0
+    lib = _lib.load()
+    assert lib.ggml_qpu_m1_weight_registered(None) == 0
+    assert lib.ggml_qpu_m1_cpu_columns_for(None) == 0
+
+
+def test_q4_0_linear_k_limits_per_row_count_before_launch() -> None:
+    # Four rows at K = 32768 need ~192 KB of LDS (> the 160 KB of a workgroup):
+    # rejected with CAPABILITY_MISSING before anything is enqueued.
+    lib = _lib.load()
+    blocks = 32768 // 32
+    status = lib.qxt_ggml_q4_0_q8_0_linear(FAKE, blocks * 34, FAKE, blocks * 18, FAKE, 64, 4, blocks, 0, 0, 16, None)
+    assert status == _lib.CAPABILITY_MISSING
+    assert "LDS" in _lib.last_error() and "4 rows" in _lib.last_error()

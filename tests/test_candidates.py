@@ -53,7 +53,7 @@ def test_registry_round_trips_winners_and_slower_candidates(tmp_path) -> None:
                                       shape_class="llama-h2048-decode")
     assert CandidateRegistry.combine(CandidateRegistry((winning,)), CandidateRegistry((slower,))).records == (
         winning, slower)
-    with pytest.raises(ValueError, match="already registered"):
+    with pytest.raises(ValueError, match="duplicate candidate name"):
         CandidateRegistry((winning, winning))
 
 
@@ -103,18 +103,18 @@ def test_registry_loads_older_schemas_and_qpu_records() -> None:
     (record,) = registry.records
     assert record.placement == "qpu" and record.performance.cpu_seconds == (0.002,)
     assert registry.to_dict()["records"][0]["placement"] == "qpu"
-    with pytest.raises(ValueError, match="unsupported candidate registry schema"):
+    with pytest.raises(ValueError, match="schema_version must be 1, 2 or 3"):
         CandidateRegistry.from_dict({"schema_version": 4, "records": []})
-    with pytest.raises(ValueError, match="must be a list"):
+    with pytest.raises(ValueError, match="must be a JSON list"):
         CandidateRegistry.from_dict({"schema_version": 3, "records": {}})
     broken = json.loads(json.dumps(payload))
     broken["records"][0]["status"] = "promoted"
-    with pytest.raises(ValueError, match="invalid record"):
+    with pytest.raises(ValueError, match="is malformed"):
         CandidateRegistry.from_dict(broken)
 
 
 def test_evidence_gates() -> None:
-    with pytest.raises(ValueError, match="measured or fused win"):
+    with pytest.raises(ValueError, match="needs correctness evidence and a measured win"):
         _linear("slow", "1x16x16", 0.0099)  # 1.01x: below the 5 % gate
     assert _linear("fast", "1x16x16", 0.0095).performance.measured_win  # 1.053x
     fused = CandidateRecord("fused", "linear", W8A8_DTYPE, W8A8_LAYOUT, "1x16x16", "h",
@@ -125,19 +125,19 @@ def test_evidence_gates() -> None:
         CandidateRecord("nan", "linear", W8A8_DTYPE, W8A8_LAYOUT, "1x16x16", "h", CandidateStatus.SUPPORTED_WIN,
                         CorrectnessEvidence("numpy", 1, False, 1.0, 1.0, 1.0, 1.0, nan_count=1),
                         PerformanceEvidence("torch", (0.002,), (0.001,)))
-    with pytest.raises(ValueError, match="failure reason"):
+    with pytest.raises(ValueError, match="needs a reason"):
         CandidateRecord("bad", "linear", W8A8_DTYPE, W8A8_LAYOUT, "s", "h", CandidateStatus.QUARANTINED_INCORRECT)
-    with pytest.raises(ValueError, match="require partition evidence"):
+    with pytest.raises(ValueError, match="needs partition evidence"):
         _linear("h", "1x16x16", 0.001, placement="hybrid")
-    with pytest.raises(ValueError, match="only hybrid"):
+    with pytest.raises(ValueError, match="hybrid records only"):
         _linear("g", "1x16x16", 0.001, partition=PartitionEvidence("rows", 16, 32, 16))
     with pytest.raises(ValueError, match="placement must be"):
         _linear("x", "1x16x16", 0.001, placement="npu")
-    with pytest.raises(ValueError, match="both CPU and QPU"):
+    with pytest.raises(ValueError, match="both partitions must be non-empty"):
         PartitionEvidence("rows", 32, 32, 16)
     with pytest.raises(ValueError, match="alignment"):
         PartitionEvidence("outputs", 8, 32, 16)
-    with pytest.raises(ValueError, match="positive"):
+    with pytest.raises(ValueError, match="> 0 seconds"):
         PerformanceEvidence("torch", (0.0,), (0.001,))
     with pytest.raises(ValueError, match="cosine"):
         QualityEvidence("numpy", 0.1, 1.5)
@@ -196,3 +196,30 @@ def test_dispatch_rejections() -> None:
         select_w8a8_dispatch(vc7_only, batch=4, features=16, outputs=16)
     with pytest.raises(ValueError, match="GPU candidate"):
         select_w8a8_dispatch(vc7_only, batch=4, features=16, outputs=16, placement=Placement.GPU)
+
+
+def test_archive_format_is_preserved_key_for_key() -> None:
+    # A schema-3 archive in the reference's layout loads and saves back to the
+    # same JSON (every field, nested evidence objects, tuples as lists).
+    record = {
+        "name": "w8a8-rows", "operation": "linear", "dtype": W8A8_DTYPE, "layout": W8A8_LAYOUT,
+        "shape_class": "64x1024x2816", "source_hash": "f00d", "status": "supported-win", "reason": "",
+        "placement": "hybrid", "kernels": ["a", "b"],
+        "correctness": {"reference": "numpy", "cases": 3, "exact": True, "max_abs_error": 0.0,
+                        "mean_abs_error": 0.0, "p99_abs_error": 0.0, "max_relative_error": 0.0,
+                        "saturation_count": 0, "nan_count": 0, "inf_count": 0},
+        "performance": {"cpu_reference": "torch", "cpu_seconds": [0.003, 0.002], "candidate_seconds": [0.001],
+                        "fused_model_win": False, "host_prep_seconds": [], "kernel_seconds": [0.0005],
+                        "cold_start_seconds": [], "dequantization_seconds": [], "same_contract_reference": "",
+                        "same_contract_seconds": []},
+        "partition": {"axis": "rows", "qpu_units": 32, "total_units": 64, "alignment": 16},
+        "quality": {"reference": "fp32", "normalized_rmse": 0.01, "cosine_similarity": 0.999,
+                    "max_abs_error": 0.1, "mean_abs_error": 0.01, "p99_abs_error": 0.05, "nan_count": 0,
+                    "inf_count": 0, "top1_agreement": None},
+    }
+    payload = {"schema_version": 3, "records": [record]}
+    registry = CandidateRegistry.from_dict(json.loads(json.dumps(payload)))
+    assert json.dumps(registry.to_dict(), sort_keys=True) == json.dumps(payload, sort_keys=True)
+    assert registry.records[0].partition.trailing == 32
+    with pytest.raises(ValueError, match="unknown keys"):
+        CandidateRegistry.from_dict({"schema_version": 2, "records": [dict(record, promoted=True)]})

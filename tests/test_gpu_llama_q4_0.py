@@ -224,3 +224,97 @@ def test_repack_weight_format_requires_whole_groups() -> None:
         status, handle = LlamaQ4_0Linear.prepare_status(
             ctx, np.ascontiguousarray(wq[:46]), weight_format=FORMAT_REPACK_4X4, **_desc(wq, k=64, n=46, rows=1, count=32))
         assert status == _lib.INVALID_ARGUMENT and not handle.value
+
+
+def test_prepare_rejects_k_the_submit_path_cannot_run_and_runs_k14336_at_four_rows() -> None:
+    rng = np.random.default_rng(7300)
+    with LlamaContext() as ctx:
+        k, n = 32768, 32  # four rows at K = 32768 exceed a workgroup's LDS
+        weight = np.zeros((n, k // 32, 18), np.uint8)
+        status, handle = LlamaQ4_0Linear.prepare_status(ctx, weight, **_desc(weight, k=k, n=n, rows=4))
+        assert status == _lib.CAPABILITY_MISSING and not handle.value
+        assert "LDS" in ctx.last_error
+        status, handle = LlamaQ4_0Linear.prepare_status(ctx, weight, **_desc(weight, k=k, n=n, rows=1))
+        assert status == _lib.OK  # one row fits
+        _lib.load().qxt_llama_q4_0_linear_destroy(handle)
+
+        k, n, rows = 14336, 256, 4
+        w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+        x = rng.standard_normal((rows, k), dtype=np.float32)
+        wq, xq = oracle.quantize_q4_0_blocks(w), oracle.quantize_q8_0_blocks(x)
+        with LlamaQ4_0Linear(ctx, wq, **_desc(wq, k=k, n=n, rows=rows)) as linear:
+            destination = np.full((rows, n), SENTINEL, dtype=np.float32)
+            linear.execute(Execution(xq, destination, 0, n))
+            np.testing.assert_array_equal(destination, oracle.q4_0_q8_0_reference(xq, wq))
+
+
+def test_cpu_fallback_after_a_failed_wait_computes_nothing() -> None:
+    # The reference's M=1 hook calls the fallback after a failed wait
+    # (ggml-qpu-up-inline.cpp:379-388); here it reports CAPABILITY_MISSING and
+    # the destination keeps its bytes.
+    g = load_golden("kat_q4_0_m1")
+    act, weight = g["activation"], g["weight"]
+    rows, blocks, n = act.shape[0], act.shape[1], weight.shape[0]
+    with LlamaContext() as ctx, LlamaQ4_0Linear(ctx, weight, **_desc(weight, k=blocks * 32, n=n, rows=rows)) as linear:
+        destination = np.full((rows, n), -777.0, dtype=np.float32)
+        ctx.set_failure_mask(_lib.FAIL_WAIT)
+        status, submission = linear.submit_status(Execution(act, destination, 0, n))
+        assert status == _lib.OK
+        status, _ = submission.wait_status()
+        assert status == _lib.TIMEOUT
+        assert submission.cpu_fallback_status() == _lib.CAPABILITY_MISSING
+        assert "no CPU compute path" in ctx.last_error
+        submission.destroy()
+        np.testing.assert_array_equal(destination, -777.0)
+
+
+def test_ggml_m1_hooks_register_by_name_and_execute(monkeypatch) -> None:
+    # Patch 0002's call sequence: set_tensor registers native Q4_0 rows by
+    # tensor name; forward_mul_mat executes one Q8_0 row (native, or passed
+    # with INTER_SIZE 4 / 8 as CPU_REPACK does for a single row) and asks how
+    # many columns the CPU must still compute.
+    from qpu_xla_amd import ggml_hooks
+
+    monkeypatch.setenv("GGML_QPU_M1_INLINE", "1")
+    monkeypatch.setenv("GGML_QPU_M1_TENSORS", "ffn_up,attn_k")
+    monkeypatch.setenv("GGML_QPU_TELEMETRY", "0")
+    ggml_hooks.release()
+    rng = np.random.default_rng(0)
+    try:
+        shapes = {"blk.3.ffn_up.weight": (2048, 5632), "blk.3.attn_k.weight": (2048, 256)}
+        cases = {}
+        for name, (k, n) in shapes.items():
+            w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+            x = rng.standard_normal((1, k), dtype=np.float32)
+            wq, xq = oracle.quantize_q4_0_blocks(w), oracle.quantize_q8_0_blocks(x)
+            cases[name] = (k, n, wq, xq, oracle.q4_0_q8_0_reference(xq, wq)[0])
+            assert ggml_hooks.register_q4_0(name, wq, k, n)
+            assert ggml_hooks.register_q4_0(name, wq, k, n)  # already registered
+            assert ggml_hooks.weight_registered(name)
+        assert not ggml_hooks.register_q4_0("blk.3.ffn_down.weight", cases["blk.3.attn_k.weight"][2], 2048, 256)
+        assert not ggml_hooks.weight_registered("blk.3.ffn_down.weight")
+        base = ggml_hooks.dispatch_count()
+        for interleave in (0, 4, 8):
+            for name, (k, n, wq, xq, want) in cases.items():
+                destination = np.full(n, np.nan, dtype=np.float32)
+                assert ggml_hooks.execute(name, xq, destination, k, n, interleave)
+                np.testing.assert_array_equal(destination, want)
+                assert ggml_hooks.cpu_columns_for(name) == 0
+                assert ggml_hooks.cpu_columns_for("blk.9.attn_q.weight") == 0
+        assert ggml_hooks.dispatch_count() == base + 6
+
+        k, n, wq, xq, want = cases["blk.3.ffn_up.weight"]
+        destination = np.full(n, -5.0, dtype=np.float32)
+        assert not ggml_hooks.execute("blk.3.ffn_up.weight", xq, destination, k, n + 16)  # shape mismatch
+        assert not ggml_hooks.execute("blk.3.ffn_up.weight", xq, destination, k, n, rows=2)
+        assert not ggml_hooks.execute("blk.3.ffn_up.weight", xq[:, :10], destination, k, n)  # short activation
+        np.testing.assert_array_equal(destination, -5.0)
+        assert ggml_hooks.cpu_columns_for("blk.3.ffn_up.weight") == n  # the CPU computes every column
+        monkeypatch.setenv("GGML_QPU_M1_INLINE", "0")
+        assert not ggml_hooks.execute("blk.3.ffn_up.weight", xq, destination, k, n)
+        assert ggml_hooks.cpu_columns_for("blk.3.ffn_up.weight") == n
+        np.testing.assert_array_equal(destination, -5.0)
+        assert ggml_hooks.dispatch_count() == base + 6
+    finally:
+        ggml_hooks.release()
+    assert not ggml_hooks.weight_registered("blk.3.ffn_up.weight")

@@ -360,6 +360,8 @@ def test_lane_pack_kernel_matches_the_layout_definition(n: int, blocks: int) -> 
     (1, 5632, 2048, 16, 2032),  # a column range starting inside a lane group
     (2, 256, 37, 5, 31),        # a partial last group, any column range
     (17, 512, 64, 0, 64),       # rows beyond one MFMA-free row group
+    (4, 14336, 1024, 0, 1024),  # K = 14336 at four rows: one-column tiles above 64 KB of LDS
+    (8, 14336, 512, 16, 496),   # two row groups at K = 14336
 ])
 def test_lane_linear_bit_exact_against_oracle(rows: int, k: int, n: int, wcol0: int, ncols: int) -> None:
     rng = np.random.default_rng(5000 + rows + n)
@@ -408,3 +410,56 @@ def test_lane_entry_points_validate_before_launching() -> None:
     status = lib.qxt_ggml_q4_0_q8_0_linear_lanes(act.data_ptr(), 272, lanes.packed.data_ptr(), 8, out.data_ptr(), 64,
                                                   1, 8, 4, 0, 8, None)
     assert status == _lib.INVALID_ARGUMENT and "past the packed matrix" in _lib.last_error()
+
+
+def test_cfg3_headline_step_lane_batch_through_the_prepass_bit_exact() -> None:
+    # The exact launch bench.py times for cfg3: all 154 TinyLlama decode
+    # linears (22 layers x q, k, v, o, gate, up, down) as one batch over
+    # lane-layout weights with fp32 activations, so the batch runs the Q8_0
+    # pre-pass launch (> 1024 work items) before the linear grid.  Every
+    # linear's output is checked against the oracle, on two launches.
+    from qpu_xla_amd.kernels.quantize import quantize_q4_0
+
+    layer = (("q", 2048, 2048), ("k", 2048, 256), ("v", 2048, 256), ("o", 2048, 2048),
+             ("gate", 2048, 5632), ("up", 2048, 5632), ("down", 5632, 2048))
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3)
+    tasks, weights, inputs = [], [], []
+    for _ in range(22):
+        for _name, k, n in layer:
+            w = torch.randn((n, k), generator=gen, device="cuda", dtype=torch.float32) * 0.02
+            wq = quantize_q4_0(w)
+            del w
+            x = torch.randn((1, k), generator=gen, device="cuda", dtype=torch.float32)
+            y = torch.full((1, n), float("nan"), device="cuda")
+            tasks.append({"x": x, "weight": q4.pack_ggml_q4_0_lane_weights(wq), "destination": y})
+            weights.append(wq)
+            inputs.append(x)
+    with q4.Q4_0LinearBatch(tasks) as batch:
+        assert batch.task_count == 154 and batch.work_items > 1024
+        for launch in range(2):
+            for t in tasks:
+                t["destination"].fill_(float("nan"))
+            torch.cuda.synchronize()
+            with _lib.launch_timing() as timing:
+                batch.launch()
+                torch.cuda.synchronize()
+            assert [name for name, _ in timing.records] == ["q8_0_prepass_kernel", "q4_0_batch_kernel"]
+            if launch == 0:
+                expected = [oracle.q4_0_q8_0_reference(oracle.quantize_q8_0_blocks(x.cpu().numpy()), wq.cpu().numpy())
+                            for x, wq in zip(inputs, weights)]
+            for i, (t, want) in enumerate(zip(tasks, expected)):
+                np.testing.assert_array_equal(t["destination"].cpu().numpy(), want, err_msg=f"linear {i}")
+
+
+@pytest.mark.parametrize("rows", [3, 4, 8])
+def test_native_linear_at_k14336_small_rows_bit_exact(rows: int) -> None:
+    # The v_dot4 kernel over native rows at a K whose activation rows need more
+    # than 64 KB of LDS at three or more rows (Llama-3-8B down projection).
+    rng = np.random.default_rng(7100 + rows)
+    k, n = 14336, 768
+    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    x = rng.standard_normal((rows, k), dtype=np.float32)
+    wq, xq = oracle.quantize_q4_0_blocks(w), oracle.quantize_q8_0_blocks(x)
+    out = q4.ggml_q4_0_q8_0_linear(dev(xq), dev(wq))
+    np.testing.assert_array_equal(out.cpu().numpy(), oracle.q4_0_q8_0_reference(xq, wq))

@@ -85,3 +85,19 @@ def test_q4_0_weights_bit_exact(rows: int, cols: int) -> None:
     w[1, :32] = np.float32(0.5)  # ties in |max|: first element wins
     w[1, 5] = np.float32(-0.5)
     np.testing.assert_array_equal(quantize_q4_0(dev(w)).cpu().numpy(), oracle.quantize_q4_0_blocks(w))
+
+
+def test_q4_0_weights_known_answer_blocks() -> None:
+    # The hand-worked blocks of ggml's rule (ties round up, first max wins,
+    # -0.0 scale of a zero block, fp16-subnormal scale, x * fl32(1/d) rather
+    # than x / d, codes from the fp32 d): codes and scale bits as literals.
+    import q4_0_kats
+
+    w, expected = q4_0_kats.kat_matrix()
+    blocks = quantize_q4_0(dev(w)).cpu().numpy()
+    np.testing.assert_array_equal(blocks, oracle.quantize_q4_0_blocks(w))
+    _, values = oracle.unpack_q4_0_blocks(blocks)
+    for b, (name, scale_bits, codes) in enumerate(expected):
+        np.testing.assert_array_equal(values[0, b].astype(np.int64) + 8, codes, err_msg=name)
+        if scale_bits is not None:
+            assert int(blocks[0, b, 0]) | (int(blocks[0, b, 1]) << 8) == scale_bits, name

@@ -242,20 +242,32 @@ def test_whole_linear_bit_exact(m: int, k: int, n: int, seed: int) -> None:
     np.testing.assert_array_equal(y, oracle.w8a8_linear_reference(x, qw, sw, bias))
 
 
-def test_cfg4_shape_sampled_rows_bit_exact() -> None:
-    # cfg4 (M=4096, K=4096, N=14336, 0.1% outlier channels x20): all rows on the GPU,
-    # the oracle on 48 sampled rows (the oracle's cost, not the kernel's, sets the sample).
+@pytest.mark.parametrize("k,n", [(4096, 14336), (14336, 4096)], ids=["gate_up", "down"])
+def test_cfg4_shape_sampled_rows_bit_exact(k: int, n: int) -> None:
+    # cfg4 (M=4096; gate_up K=4096, N=14336 and down K=14336, N=4096; seed 4;
+    # 0.1% outlier channels x20): all rows on the GPU through the 256 x 256
+    # stream kernel (112 K stages at down), the oracle on 48 sampled rows (the
+    # oracle's cost, not the kernel's, sets the sample).  Mirrors the
+    # reference's assert_array_equal at tests/test_qpu_xla_gemm_int8.py:57-92.
+    from qpu_xla_amd import _lib
+
     rng = np.random.default_rng(4)
-    m, k, n = 4096, 4096, 14336
+    m = 4096
     x = rng.standard_normal((m, k), dtype=np.float32)
     x[:, rng.choice(k, round(0.001 * k), replace=False)] *= np.float32(20.0)
     w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
     bias = (rng.standard_normal(n, dtype=np.float32) * np.float32(0.1)).astype(np.float32)
     weight = quantize_per_output_channel_int8(dev(w))
-    y = w8a8_linear(dev(x), weight, dev(bias))
+    xd, bd = dev(x), dev(bias)
+    torch.cuda.synchronize()
+    with _lib.launch_timing() as timing:
+        y = w8a8_linear(xd, weight, bd)
+    assert "w8a8_gemm_stream_kernel" in [name for name, _ in timing.records]
     rows = np.sort(rng.choice(m, 48, replace=False))
     rows[0], rows[-1] = 0, m - 1
     qw, sw = oracle.quantize_per_output_channel_int8(w)
+    np.testing.assert_array_equal(weight.values.cpu().numpy(), qw)
+    np.testing.assert_array_equal(weight.scales.cpu().numpy(), sw)
     expected = oracle.w8a8_linear_reference(x[rows], qw, sw, bias)
     np.testing.assert_array_equal(y[torch.from_numpy(rows).cuda()].cpu().numpy(), expected)
 

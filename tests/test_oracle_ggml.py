@@ -8,6 +8,7 @@ import numpy as np
 import pytest
 
 import oracle
+import q4_0_kats
 from conftest import load_golden
 
 
@@ -150,8 +151,87 @@ def test_q8_0_blocks_equal_split_form() -> None:
     np.testing.assert_array_equal(blocks[..., 2:].reshape(codes.shape).view(np.int8), codes)
 
 
-def test_q4_0_quantiser_invariants_parity_unpinned_vs_ggml() -> None:
-    # Only the BASELINE formula's invariants are checked (ggml is not vendored).
+@pytest.mark.parametrize("kat", q4_0_kats.kat_blocks(), ids=lambda k: k[0])
+def test_q4_0_quantiser_known_answer_blocks(kat) -> None:
+    # Literal codes worked by hand from ggml's quantize_row_q4_0_ref rule.
+    name, values, scale_bits, codes, fill = kat
+    blocks = oracle.quantize_q4_0_blocks(values[None, :])
+    d, v = oracle.unpack_q4_0_blocks(blocks)
+    got = v[0, 0].astype(np.int64) + 8
+    want = np.full(32, fill, dtype=np.int64)
+    for index, code in codes.items():
+        want[index] = code
+    np.testing.assert_array_equal(got, want, err_msg=name)
+    bits = int(blocks[0, 0, 0]) | (int(blocks[0, 0, 1]) << 8)
+    if scale_bits is not None:
+        assert bits == scale_bits, f"{name}: fp16 scale bits {bits:#06x}, want {scale_bits:#06x}"
+
+
+@pytest.mark.parametrize("kat", q4_0_kats.kat_blocks(), ids=lambda k: k[0])
+def test_q4_0_known_answer_blocks_agree_with_exact_arithmetic(kat) -> None:
+    # The literal codes themselves, re-derived with exact rationals and explicit
+    # round-to-fp32 steps (independent of NumPy's float32 arithmetic).
+    name, values, _, codes, fill = kat
+    d, exact = q4_0_kats.exact_codes(values)
+    want = [codes.get(i, fill) for i in range(32)]
+    assert exact == want, name
+    blocks = oracle.quantize_q4_0_blocks(values[None, :])
+    assert float(np.float16(float(d))) == float(oracle.unpack_q4_0_blocks(blocks)[0][0, 0])
+
+
+def test_q4_0_separators_distinguish_the_plausible_mistakes() -> None:
+    # The two separator blocks really separate: dividing by d, or using the
+    # fp16-rounded d, changes their second code (checked in exact arithmetic).
+    from fractions import Fraction
+
+    rn = q4_0_kats._rn32
+    for name, values, _, codes, _ in q4_0_kats.kat_blocks():
+        if name not in ("reciprocal_not_division", "fp32_scale_not_fp16"):
+            continue
+        m, x = Fraction(float(values[0])), Fraction(float(values[1]))
+        d = rn(m / -8)
+        if name == "reciprocal_not_division":
+            wrong = min(15, int(rn(rn(x / d) + Fraction(17, 2))))
+        else:
+            d16 = Fraction(float(np.float16(float(d))))
+            wrong = min(15, int(rn(rn(x * rn(1 / d16)) + Fraction(17, 2))))
+        assert wrong != codes[1], name
+
+
+def test_q4_0_quantiser_random_blocks_match_exact_arithmetic() -> None:
+    rng = np.random.default_rng(77)
+    w = rng.standard_normal((6, 128), dtype=np.float32) * np.float32(0.02)
+    w[2, 32:64] *= np.float32(1e-3)  # small scales
+    blocks = oracle.quantize_q4_0_blocks(w)
+    d, v = oracle.unpack_q4_0_blocks(blocks)
+    for r in range(w.shape[0]):
+        for b in range(w.shape[1] // 32):
+            exact_d, exact = q4_0_kats.exact_codes(w[r, 32 * b : 32 * b + 32])
+            np.testing.assert_array_equal(v[r, b].astype(np.int64) + 8, exact)
+            assert float(np.float16(float(exact_d))) == float(d[r, b])
+
+
+def test_q4_0_quantiser_half_step_reconstruction_bound() -> None:
+    # Round-half-up of x/d: every element not clamped at code 15 lies within
+    # half a step of its code (in units of the fp32 d the codes were made with);
+    # trunc(x/d + 8) would miss this by up to a whole step.
+    rng = np.random.default_rng(9)
+    w = rng.standard_normal((16, 512), dtype=np.float32) * np.float32(0.02)
+    blocks = oracle.quantize_q4_0_blocks(w)
+    _, v = oracle.unpack_q4_0_blocks(blocks)
+    g = w.reshape(16, 16, 32).astype(np.float64)
+    first = np.abs(g).argmax(axis=2)
+    d32 = np.take_along_axis(g, first[..., None], axis=2) / -8.0  # exact: division by 8
+    ratio = g / d32
+    codes = v.astype(np.int64) + 8
+    inner = codes < 15
+    err = np.abs(ratio - (codes - 8))
+    assert np.all(err[inner] <= 0.5 + 1e-5)
+    assert np.all(ratio[~inner] >= 6.5 - 1e-5)  # clamped elements sit in the top half step or above
+    np.testing.assert_array_equal(np.take_along_axis(codes, first[..., None], axis=2), 0)
+
+
+def test_q4_0_quantiser_invariants() -> None:
     rng = np.random.default_rng(9)
     w = rng.standard_normal((8, 256), dtype=np.float32) * np.float32(0.02)
     w[3, :32] = 0.0
