@@ -341,6 +341,20 @@ int qxt_w8a8_linear(const float *x, size_t ldx, int8_t *qa, size_t ldqa, float *
                     float *y, size_t ldy, uint32_t m, uint32_t n, uint32_t k,
                     uint32_t weight_layout, uint32_t flags, void *stream);
 
+/* qxt_w8a8_linear without workspace arguments and without any allocation:
+ * the quantised activation rows and row scales live in a static device array
+ * of the library (64 MiB of int8 rows + 256 KiB of scales per GPU, held from
+ * the library's first use on that GPU until the process ends).  Limits: m <=
+ * 65,536 and m * k <= 64 MiB (2^26), else QXT_INVALID_ARGUMENT before anything
+ * is enqueued.  Same result as qxt_w8a8_linear bit for bit.  Every call on one
+ * GPU shares that GPU's array, so calls that overlap on one GPU (other streams,
+ * other threads) race; order them on one stream.  No counterpart in the
+ * reference: for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). */
+int qxt_w8a8_linear_noalloc(const float *x, size_t ldx, const void *w, size_t ldw, const float *column_scales,
+                            const float *bias, float *y, size_t ldy, uint32_t m, uint32_t n, uint32_t k,
+                            uint32_t weight_layout, uint32_t flags, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

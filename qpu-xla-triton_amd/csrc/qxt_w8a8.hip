@@ -21,7 +21,9 @@
 // exact integer sum does not depend on how the chunk is ordered) and receives
 // D[8 * (r / 4) + 4 * (l / 32) + r % 4][l % 32] in accumulator register r.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
+#include <vector>
 
 #include "qxt_common.h"
 
@@ -983,6 +985,43 @@ int validate_epilogue(const float *sa, const float *sw, const float *bias, const
     return QXT_OK;
 }
 
+// ------------------------------------------------- static workspace (no allocation)
+//
+// qxt_w8a8_linear_noalloc keeps the quantised activation rows (int8, row
+// stride k) and their fp32 row scales in this array instead of caller or
+// library allocations.  Each GPU holds its own copy from the moment the
+// library's code object is loaded on it until the process ends; every call
+// on a GPU reuses that GPU's copy.  Nothing in it has to start at zero: the
+// row quantiser writes every byte a call reads.
+constexpr size_t kScratchRowBytes = size_t(64) << 20;   // int8 activation rows: m * k <= 64 MiB
+constexpr size_t kScratchScaleBytes = size_t(256) << 10;  // fp32 row scales: m <= 65,536
+constexpr uint32_t kScratchMaxRows = kScratchScaleBytes / sizeof(float);
+
+static __device__ __align__(256) uint8_t scratch[kScratchRowBytes + kScratchScaleBytes];
+
+// Device address of `scratch`, looked up once per device with that device
+// current.  Host code never passes the array's name to a kernel or copy: on
+// the host that name is only a stand-in for the symbol, not a device address.
+int scratch_address(uint8_t **out) {
+    static std::mutex mutex;
+    static std::vector<uint8_t *> by_device;
+    int device = -1;
+    if (hipGetDevice(&device) != hipSuccess || device < 0)
+        return fail(QXT_DEVICE_UNAVAILABLE, "w8a8 linear noalloc: no current HIP device");
+    std::lock_guard<std::mutex> guard(mutex);
+    if (by_device.size() <= static_cast<size_t>(device)) by_device.resize(device + 1, nullptr);
+    if (by_device[device] == nullptr) {
+        void *address = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || address == nullptr)
+            return fail(QXT_DEVICE_UNAVAILABLE, "w8a8 linear noalloc: workspace address on device %d: %s", device,
+                        hipGetErrorString(err));
+        by_device[device] = static_cast<uint8_t *>(address);
+    }
+    *out = by_device[device];
+    return QXT_OK;
+}
+
 }  // namespace
 }  // namespace qxt
 
@@ -1067,6 +1106,24 @@ int qxt_w8a8_linear(const float *x, size_t ldx, int8_t *qa, size_t ldqa, float *
     GemmArgs args{qa, ldqa, static_cast<const uint8_t *>(w), ldw, nullptr, 0, sa, column_scales, bias,
                   y, ldy, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k)};
     return run_gemm(args, bias != nullptr ? EPI_DEQUANT_BIAS : EPI_DEQUANT, weight_layout, as_stream(stream));
+}
+
+int qxt_w8a8_linear_noalloc(const float *x, size_t ldx, const void *w, size_t ldw, const float *column_scales,
+                            const float *bias, float *y, size_t ldy, uint32_t m, uint32_t n, uint32_t k,
+                            uint32_t weight_layout, uint32_t flags, void *stream) {
+    if (m == 0 || k == 0 || k % 16)
+        return fail(QXT_INVALID_ARGUMENT, "w8a8 linear noalloc: m > 0 and k a positive multiple of 16 required");
+    if (m > kScratchMaxRows || static_cast<uint64_t>(m) * k > kScratchRowBytes)
+        return fail(QXT_INVALID_ARGUMENT,
+                    "w8a8 linear noalloc: m = %u rows of k = %u exceed the static workspace (m <= %u, m * k <= %zu)",
+                    m, k, kScratchMaxRows, kScratchRowBytes);
+    uint8_t *base = nullptr;
+    int rc = scratch_address(&base);
+    if (rc != QXT_OK) return rc;
+    int8_t *qa = reinterpret_cast<int8_t *>(base);
+    float *sa = reinterpret_cast<float *>(base + kScratchRowBytes);
+    return qxt_w8a8_linear(x, ldx, qa, k, sa, w, ldw, column_scales, bias, y, ldy, m, n, k, weight_layout, flags,
+                           stream);
 }
 
 }  // extern "C"

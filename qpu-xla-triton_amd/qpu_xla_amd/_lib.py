@@ -178,6 +178,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "qxt_w8a8_gemm_dequantize": (c_int, [_P, _SZ, _P, _SZ, _P, _P, _P, _P, _SZ, _U, _U, _U, _U, _P]),
     "qxt_w8a8_dequantize": (c_int, [_P, _SZ, _P, _P, _P, _P, _SZ, _U, _U, _P]),
     "qxt_w8a8_linear": (c_int, [_P, _SZ, _P, _SZ, _P, _P, _SZ, _P, _P, _P, _SZ, _U, _U, _U, _U, _U, _P]),
+    "qxt_w8a8_linear_noalloc": (c_int, [_P, _SZ, _P, _SZ, _P, _P, _P, _SZ, _U, _U, _U, _U, _U, _P]),
     "qxt_llama_context_create": (c_int, [POINTER(LlamaContextConfig), POINTER(c_void_p)]),
     "qxt_llama_context_destroy": (None, [_P]),
     "qxt_llama_context_last_error": (c_char_p, [_P]),

@@ -222,3 +222,14 @@ def test_q4_0_linear_k_limits_per_row_count_before_launch() -> None:
     status = lib.qxt_ggml_q4_0_q8_0_linear(FAKE, blocks * 34, FAKE, blocks * 18, FAKE, 64, 4, blocks, 0, 0, 16, None)
     assert status == _lib.CAPABILITY_MISSING
     assert "LDS" in _lib.last_error() and "4 rows" in _lib.last_error()
+
+
+def test_w8a8_linear_noalloc_rejects_sizes_beyond_its_workspace_before_launch() -> None:
+    lib = _lib.load()
+    # m * k = 4096 * 16400 bytes > 64 MiB; m = 65537 rows > 65,536 scales.
+    status = lib.qxt_w8a8_linear_noalloc(FAKE, 16400 * 4, FAKE, 16400, FAKE, None, FAKE, 64, 4096, 16, 16400, 0, 0, None)
+    assert status == _lib.INVALID_ARGUMENT and "static workspace" in _lib.last_error()
+    status = lib.qxt_w8a8_linear_noalloc(FAKE, 64, FAKE, 16, FAKE, None, FAKE, 64, 65537, 16, 16, 0, 0, None)
+    assert status == _lib.INVALID_ARGUMENT and "static workspace" in _lib.last_error()
+    status = lib.qxt_w8a8_linear_noalloc(FAKE, 64, FAKE, 16, FAKE, None, FAKE, 64, 4, 16, 24, 0, 0, None)
+    assert status == _lib.INVALID_ARGUMENT and "multiple of 16" in _lib.last_error()
