@@ -83,6 +83,27 @@ struct Q4Item {
 
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 
+// Batch kernels read their tensor pointers from a device table, so the
+// compiler cannot tell they address global memory and would emit FLAT
+// loads.  A FLAT load also counts against the LDS counter, which turns every
+// later wait for an LDS access into a wait for all outstanding weight loads
+// (activation staging then starts only after the weights have landed).
+// Every tensor access goes through a global-address-space pointer instead.
+#define QXT_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ const QXT_GLOBAL T *global_in(const void *p) {
+    return (const QXT_GLOBAL T *)p;
+}
+template <typename T>
+__device__ __forceinline__ QXT_GLOBAL T *global_out(void *p) {
+    return (QXT_GLOBAL T *)p;
+}
+__device__ __forceinline__ float4 load_float4(const void *p) {
+    const v4u raw = *global_in<v4u>(p);
+    return make_float4(__uint_as_float(raw[0]), __uint_as_float(raw[1]), __uint_as_float(raw[2]),
+                       __uint_as_float(raw[3]));
+}
+
 // LDS geometry (in 32-bit words) for a row group of MR rows.
 struct Q4Lds {
     int aq_row;  // activation int8 words per row: 8 per block + 4 pad per 8 blocks
@@ -137,6 +158,72 @@ __device__ __forceinline__ int block_dot(const uint32_t (&qs)[4], const int *aq,
     return s - 8 * asum;
 }
 
+// Quantise element chunk e (float4 v: elements 4 (e % 8) .. of block e / 8 of
+// row r) by the rule of q8_0_prepass_kernel -- 8 lanes per block, the dots use
+// the fp16-rounded d -- into the LDS activation of row r; nothing is stored
+// when `store` is false.  The 8 lanes of a block must be active together.
+__device__ __forceinline__ void quantise_chunk(const float4 &v, int r, int rem, int *aq, int *ad, const Q4Lds &geo,
+                                               bool store = true) {
+    const int b = rem >> 3, l8 = rem & 7;
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
+    const float d = amax / 127.0f;
+    const float inv = (d != 0.0f) ? 1.0f / d : 0.0f;
+    const int q0 = clamp127(rintf(v.x * inv)), q1 = clamp127(rintf(v.y * inv));
+    const int q2 = clamp127(rintf(v.z * inv)), q3 = clamp127(rintf(v.w * inv));
+    int sum = q0 + q1 + q2 + q3;
+    sum += __shfl_xor(sum, 1, 8);
+    sum += __shfl_xor(sum, 2, 8);
+    sum += __shfl_xor(sum, 4, 8);
+    if (!store) return;
+    aq[r * geo.aq_row + aq_index(b, l8)] = static_cast<int>(pack_bytes(q0, q1, q2, q3));
+    if (l8 == 0) {
+        ad[r * geo.ad_row + ad_index(b)] = __float_as_int(half_bits_to_float(float_to_half_bits(d)));
+        ad[r * geo.ad_row + ad_index(b) + 1] = sum;
+    }
+}
+
+// A one-row fp32 activation of K <= kMaxPrefetchChunks * 4 * kThreads
+// (6144) is requested before the weights, PC 16-byte chunks per thread, so
+// that its quantisation waits only for its own loads: a wave's loads
+// complete in order, and a row requested after the weights would arrive
+// only after all of them.
+constexpr int kMaxPrefetchChunks = 6;
+
+// Chunks per thread that hold a one-row fp32 activation of `t` (2, 4 or 6),
+// or 0 when the task does not qualify.
+__host__ __device__ inline int prefetch_chunks(const Q4Task &t) {
+    if (t.x == nullptr || t.rows != 1) return 0;
+    const int chunks = (t.blocks * 8 + kThreads - 1) / kThreads;
+    return chunks <= 2 ? 2 : chunks <= 4 ? 4 : chunks <= kMaxPrefetchChunks ? kMaxPrefetchChunks : 0;
+}
+
+template <int PC>
+__device__ __forceinline__ void prefetch_row(const Q4Task &t, float4 (&xv)[PC]) {
+    const int total = t.blocks * 8;
+#pragma unroll
+    for (int u = 0; u < PC; ++u) {
+        // Unconditional loads (lanes past the row re-read its last chunk, unused).
+        const int e = min(u * kThreads + static_cast<int>(threadIdx.x), total - 1);
+        xv[u] = load_float4(reinterpret_cast<const uint8_t *>(t.x) + e * 16);
+    }
+}
+
+template <int PC>
+__device__ __forceinline__ void quantise_row(const Q4Task &t, const float4 (&xv)[PC], int *aq, int *ad,
+                                             const Q4Lds &geo) {
+    const int total = t.blocks * 8;  // a multiple of 8: whole 8-lane groups
+    // Every lane quantises (lanes past the row work on a re-read chunk and
+    // store nothing), so no load is sunk into a branch behind the weights.
+#pragma unroll
+    for (int u = 0; u < PC; ++u) {
+        const int e = u * kThreads + threadIdx.x;
+        quantise_chunk(xv[u], 0, min(e, total - 1), aq, ad, geo, e < total);
+    }
+}
+
 // Stage the activation rows r0 .. r0+MR-1 of `t` into LDS (rows >= t.rows become zeros).
 template <int MR>
 __device__ __forceinline__ void stage_activation(const Q4Task &t, int r0, int *aq, int *ad, const Q4Lds &geo) {
@@ -156,33 +243,15 @@ __device__ __forceinline__ void stage_activation(const Q4Task &t, int r0, int *a
                 v[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 const int r = e / (B * 8);
                 if (e < total && r0 + r < t.rows)
-                    v[u] = *reinterpret_cast<const float4 *>(reinterpret_cast<const uint8_t *>(t.x) +
-                                                             (r0 + r) * t.x_stride + (e - r * B * 8) * 16);
+                    v[u] = load_float4(reinterpret_cast<const uint8_t *>(t.x) + (r0 + r) * t.x_stride +
+                                       (e - r * B * 8) * 16);
             }
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int e = base + u * kThreads + threadIdx.x;
                 if (e >= total) break;
                 const int r = e / (B * 8);
-                const int rem = e - r * B * 8;
-                const int b = rem >> 3, l8 = rem & 7;
-                float amax = fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w)));
-                amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
-                amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
-                amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
-                const float d = amax / 127.0f;
-                const float inv = (d != 0.0f) ? 1.0f / d : 0.0f;
-                const int q0 = clamp127(rintf(v[u].x * inv)), q1 = clamp127(rintf(v[u].y * inv));
-                const int q2 = clamp127(rintf(v[u].z * inv)), q3 = clamp127(rintf(v[u].w * inv));
-                int sum = q0 + q1 + q2 + q3;
-                sum += __shfl_xor(sum, 1, 8);
-                sum += __shfl_xor(sum, 2, 8);
-                sum += __shfl_xor(sum, 4, 8);
-                aq[r * geo.aq_row + aq_index(b, l8)] = static_cast<int>(pack_bytes(q0, q1, q2, q3));
-                if (l8 == 0) {
-                    ad[r * geo.ad_row + ad_index(b)] = __float_as_int(half_bits_to_float(float_to_half_bits(d)));
-                    ad[r * geo.ad_row + ad_index(b) + 1] = sum;
-                }
+                quantise_chunk(v[u], r, e - r * B * 8, aq, ad, geo);
             }
         }
         return;
@@ -194,8 +263,8 @@ __device__ __forceinline__ void stage_activation(const Q4Task &t, int r0, int *a
         float d = 0.0f;
         int sum = 0;
         if (r0 + r < t.rows) {
-            const uint16_t *p = reinterpret_cast<const uint16_t *>(t.act + (r0 + r) * t.act_stride +
-                                                                   static_cast<size_t>(b) * Q8_0_BYTES);
+            const QXT_GLOBAL uint16_t *p =
+                global_in<uint16_t>(t.act + (r0 + r) * t.act_stride + static_cast<size_t>(b) * Q8_0_BYTES);
             d = half_bits_to_float(p[0]);
 #pragma unroll
             for (int h = 0; h < 16; ++h) {
@@ -212,19 +281,32 @@ __device__ __forceinline__ void stage_activation(const Q4Task &t, int r0, int *a
     }
 }
 
-template <int U>
+// Weight layout of a kernel instantiation: native rows, lane layout, or
+// either (read from the task).  Separate instantiations keep the lane
+// layout's non-temporal loads from being merged with the native rows'
+// ordinary loads of the other branch.
+enum WeightLayout { kNativeRows = 0, kLaneLayout = 1, kEitherLayout = 2 };
+
+// CLAMP: every lane issues its loads, a lane past the tile re-reading the
+// tile's last unit (its registers are never used).  The loads are then
+// straight-line code, so the compiler counts them exactly and a later wait
+// for an earlier load (a prefetched activation) does not wait for these.
+// Without CLAMP, lanes past the tile skip their loads (cheaper for small
+// tiles when nothing loaded earlier is waited for).
+template <int U, int LAYOUT = kEitherLayout, bool CLAMP = false>
 __device__ __forceinline__ void load_units(const Q4Task &t, int col_base, int G, int units, int first,
                                            uint32_t (&d)[U][36]) {
 #pragma unroll
     for (int j = 0; j < U; ++j) {
-        const int u = first + j * kThreads + threadIdx.x;
-        if (u < units) {
+        const int lane_unit = first + j * kThreads + static_cast<int>(threadIdx.x);
+        const int u = CLAMP ? min(lane_unit, units - 1) : lane_unit;
+        if (CLAMP || u < units) {
             const int col = u / G;
             const int g = u - col * G;
-            if (t.lanes) {
+            if (LAYOUT == kLaneLayout || (LAYOUT == kEitherLayout && t.lanes)) {
                 const size_t unit = static_cast<size_t>(t.wcol0 + col_base + col) * G + g;
-                const v4u *src = reinterpret_cast<const v4u *>(t.w + (unit / kLaneGroup) * kGroupBytes +
-                                                               (unit % kLaneGroup) * 16);
+                const QXT_GLOBAL v4u *src =
+                    global_in<v4u>(t.w + (unit / kLaneGroup) * kGroupBytes + (unit % kLaneGroup) * 16);
 #pragma unroll
                 for (int v = 0; v < 9; ++v) {
                     const v4u x = __builtin_nontemporal_load(src + v * kLaneGroup);
@@ -234,7 +316,7 @@ __device__ __forceinline__ void load_units(const Q4Task &t, int col_base, int G,
                     d[j][4 * v + 3] = x[3];
                 }
             } else {
-                const v4u *src = reinterpret_cast<const v4u *>(
+                const QXT_GLOBAL v4u *src = global_in<v4u>(
                     t.w + static_cast<size_t>(t.wcol0 + col_base + col) * t.w_stride + static_cast<size_t>(g) * 144);
 #pragma unroll
                 for (int v = 0; v < 9; ++v) {
@@ -274,6 +356,14 @@ __global__ __launch_bounds__(kThreads) void pack_lanes_kernel(const uint8_t *__r
 // dependency stages: 128-704 items; the whole cfg3 step: 7436).
 constexpr size_t kFusedQuantItems = 1024;
 
+// Workgroups per CU below which a batch narrows its column tiles (measured
+// on MI355X, the 88-launch staged decode step of cfg3: no narrowing 0.67 ms,
+// one workgroup per CU 0.43 ms, two 0.49 ms, four and more slower still).
+#ifndef QXT_BATCH_ITEMS_PER_CU
+#define QXT_BATCH_ITEMS_PER_CU 1
+#endif
+constexpr int kBatchItemsPerCu = QXT_BATCH_ITEMS_PER_CU;
+
 struct Q8Job {
     const float *x;
     size_t x_stride;
@@ -301,7 +391,7 @@ __global__ __launch_bounds__(kThreads) void q8_0_prepass_kernel(const Q8Job *__r
     const int b = gb - row * j.blocks;
     const float *src = reinterpret_cast<const float *>(reinterpret_cast<const uint8_t *>(j.x) + row * j.x_stride) +
                        b * QK + l8 * 4;
-    const v4u raw = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(src));
+    const v4u raw = __builtin_nontemporal_load(global_in<v4u>(src));
     const float xs[4] = {__uint_as_float(raw[0]), __uint_as_float(raw[1]), __uint_as_float(raw[2]),
                          __uint_as_float(raw[3])};
     float amax = fmaxf(fmaxf(fabsf(xs[0]), fabsf(xs[1])), fmaxf(fabsf(xs[2]), fabsf(xs[3])));
@@ -316,10 +406,10 @@ __global__ __launch_bounds__(kThreads) void q8_0_prepass_kernel(const Q8Job *__r
     uint8_t *dst = j.out + (static_cast<size_t>(row) * j.blocks + b) * Q8_0_BYTES;
     const uint32_t word = pack_bytes(q[0], q[1], q[2], q[3]);
     // Block bytes 2 + 4 * l8 .. are 2-byte aligned: two half-word stores.
-    uint16_t *h = reinterpret_cast<uint16_t *>(dst + 2 + 4 * l8);
+    QXT_GLOBAL uint16_t *h = global_out<uint16_t>(dst + 2 + 4 * l8);
     h[0] = static_cast<uint16_t>(word & 0xFFFFu);
     h[1] = static_cast<uint16_t>(word >> 16);
-    if (l8 == 0) *reinterpret_cast<uint16_t *>(dst) = static_cast<uint16_t>(float_to_half_bits(d));
+    if (l8 == 0) *global_out<uint16_t>(dst) = static_cast<uint16_t>(float_to_half_bits(d));
 }
 
 // Phase 2 of the fast path for one round of U units per thread (units
@@ -366,7 +456,8 @@ __device__ __forceinline__ void compute_fast(const Q4Task &t, int col_base, int 
         for (int r = 0; r < MR; ++r) {
             if constexpr (DOTS) {
                 if (r0 + r < t.rows) {
-                    int32_t *out = t.dots + (static_cast<size_t>(r0 + r) * t.ncols + col_base + col) * B + g * 8;
+                    QXT_GLOBAL int32_t *out =
+                        global_out<int32_t>(t.dots + (static_cast<size_t>(r0 + r) * t.ncols + col_base + col) * B + g * 8);
 #pragma unroll
                     for (int i = 0; i < 8; ++i) out[i] = idots[r][i];
                 }
@@ -402,13 +493,13 @@ __device__ __forceinline__ void sum_store(const Q4Task &t, int col_base, int r0,
         } else {
             for (int b = 0; b < B; ++b) acc += c[b];
         }
-        float *out = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(t.y) + (r0 + r) * t.y_stride);
+        QXT_GLOBAL float *out = global_out<float>(reinterpret_cast<uint8_t *>(t.y) + (r0 + r) * t.y_stride);
         out[t.ocol0 + col_base + col] = acc;
     }
 }
 
 // One linear: workgroup (x, y) owns columns [x * cpw, +cpw) and rows [y * MR, +MR).
-template <int MR, int U, bool FAST, bool DOTS>
+template <int MR, int U, bool FAST, bool DOTS, int LAYOUT = kNativeRows>
 __global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Task t) {
     extern __shared__ int lds[];
     const int col_base = blockIdx.x * t.cpw;
@@ -423,7 +514,7 @@ __global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Task t) {
     const int G = FAST ? (B >> 3) : B;
     const int units = tile_cols * G;
     uint32_t wr[FAST ? U : 1][36];
-    if constexpr (FAST) load_units<U>(t, col_base, G, units, 0, wr);
+    if constexpr (FAST) load_units<U, LAYOUT>(t, col_base, G, units, 0, wr);
 
     stage_activation<MR>(t, r0, aq, ad, geo);
     __syncthreads();
@@ -434,7 +525,7 @@ __global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Task t) {
         for (int first = 0; first < units; first += U * kThreads) {
             uint32_t wn[U][36];
             const bool more = first + U * kThreads < units;
-            if (more) load_units<U>(t, col_base, G, units, first + U * kThreads, wn);
+            if (more) load_units<U, LAYOUT>(t, col_base, G, units, first + U * kThreads, wn);
             compute_fast<MR, U, DOTS>(t, col_base, r0, G, units, first, wr, aq, ad, cb, geo);
             if (more) {
 #pragma unroll
@@ -445,14 +536,14 @@ __global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Task t) {
         }
     } else if constexpr (FAST) {
         for (int first = 0; first < units; first += U * kThreads) {
-            if (first > 0) load_units<U>(t, col_base, G, units, first, wr);
+            if (first > 0) load_units<U, LAYOUT>(t, col_base, G, units, first, wr);
             compute_fast<MR, U, DOTS>(t, col_base, r0, G, units, first, wr, aq, ad, cb, geo);
         }
     } else {
         for (int u = threadIdx.x; u < units; u += kThreads) {
             const int col = u / B;
             const int b = u - col * B;
-            const uint16_t *p = reinterpret_cast<const uint16_t *>(t.w + static_cast<size_t>(t.wcol0 + col_base + col) *
+            const QXT_GLOBAL uint16_t *p = global_in<uint16_t>(t.w + static_cast<size_t>(t.wcol0 + col_base + col) *
                                                                              t.w_stride +
                                                                    static_cast<size_t>(b) * Q4_0_BYTES);
             const float dw = half_bits_to_float(p[0]);
@@ -487,7 +578,11 @@ __global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Task t) {
 // item queue round-robin with one item of weight prefetch, and 5-15 %
 // slower when the last 2-8 x CUs items are cut into halves or quarters to
 // shorten the drain.)
-template <int MR, int U>
+// PC > 0 (one-row batches whose every task gives an fp32 activation of
+// K <= 256 * 4 * PC): the activation row is requested before the weights.  A
+// compile-time choice: under a run-time branch the compiler cannot count
+// the weight loads issued after it and waits for all of them.
+template <int MR, int U, int LAYOUT, int PC>
 __global__ __launch_bounds__(kThreads) void q4_0_batch_kernel(const Q4Task *__restrict__ tasks,
                                                               const Q4Item *__restrict__ items) {
     extern __shared__ int lds[];
@@ -496,13 +591,17 @@ __global__ __launch_bounds__(kThreads) void q4_0_batch_kernel(const Q4Task *__re
     const int B = t.blocks;
     const int G = B >> 3;
     const int units = item.ncols * G;
+    static_assert(PC == 0 || MR == 1, "the activation prefetch serves one-row batches");
+    float4 xv[PC > 0 ? PC : 1];
+    if constexpr (PC > 0) prefetch_row<PC>(t, xv);
     uint32_t wr[U][36];
-    load_units<U>(t, item.col_base, G, units, 0, wr);
+    load_units<U, LAYOUT, (PC > 0)>(t, item.col_base, G, units, 0, wr);
     const Q4Lds geo(B, true);
     int *aq = lds;
     int *ad = aq + MR * geo.aq_row;
     float *cb = reinterpret_cast<float *>(ad + MR * geo.ad_row);
-    stage_activation<MR>(t, 0, aq, ad, geo);
+    if constexpr (PC > 0) quantise_row<PC>(t, xv, aq, ad, geo);
+    else stage_activation<MR>(t, 0, aq, ad, geo);
     __syncthreads();
     compute_fast<MR, U, false>(t, item.col_base, 0, G, units, 0, wr, aq, ad, cb, geo);
     __syncthreads();
@@ -511,6 +610,16 @@ __global__ __launch_bounds__(kThreads) void q4_0_batch_kernel(const Q4Task *__re
 
 // Units each thread owns per round on the fast path.
 constexpr int units_per_thread(int mr) { return mr == 1 ? 2 : 1; }
+
+// Units per thread of the activation-prefetch batch kernels (one-row tasks;
+// one unit: narrower tiles, fewer idle lanes re-reading a unit -- staged
+// decode 0.47 -> 0.43 ms against two).
+#ifndef QXT_PREFETCH_UNITS
+#define QXT_PREFETCH_UNITS 1
+#endif
+constexpr int kPrefetchUnits = QXT_PREFETCH_UNITS;
+static_assert(kPrefetchUnits >= 1 && kPrefetchUnits <= units_per_thread(1),
+              "a prefetch plan must fit the one-row batch kernel it falls back to");
 
 bool fast_path(const Q4Task &t) { return t.blocks % 8 == 0 && aligned(t.w, 16) && t.w_stride % 16 == 0; }
 
@@ -529,10 +638,11 @@ size_t lanes_bytes(uint64_t columns, uint64_t blocks) {
 // workgroup.  A K whose single-column tile exceeds kMaxLds also runs, on
 // fewer workgroups per CU, up to the whole LDS (about K = 111k at one row,
 // 55k at two, 37k at three and 27k at four rows).
-int plan_task(Q4Task &t, int mr, bool fast, bool dots, size_t *lds, int max_cpw = 1 << 30, bool wide = false) {
+int plan_task(Q4Task &t, int mr, bool fast, bool dots, size_t *lds, int max_cpw = 1 << 30, bool wide = false,
+              int upt = 0) {
     const Q4Lds geo(t.blocks, fast);
     const int units_per_col = fast ? t.blocks / 8 : t.blocks;
-    const int per_round = kThreads * (fast ? units_per_thread(mr) : 1);
+    const int per_round = kThreads * (fast ? (upt > 0 ? upt : units_per_thread(mr)) : 1);
     int cpw = units_per_col >= per_round ? 1 : per_round / units_per_col;
     if (wide) cpw = max_cpw;
     cpw = std::max(1, std::min({cpw, t.ncols, max_cpw}));
@@ -567,6 +677,11 @@ int launch_single(Q4Task t, hipStream_t stream) {
     dim3 grid((t.ncols + t.cpw - 1) / t.cpw, row_groups, 1);
     constexpr int U = units_per_thread(MR);
     const char *name = DOTS ? "q4_0_block_dots_kernel" : "q4_0_linear_kernel";
+    if constexpr (!DOTS) {
+        if (fast && t.lanes)
+            return launch(name, q4_0_linear_kernel<MR, U, true, false, kLaneLayout>, grid, dim3(kThreads), lds, stream,
+                          t);
+    }
     if (fast) return launch(name, q4_0_linear_kernel<MR, U, true, DOTS>, grid, dim3(kThreads), lds, stream, t);
     return launch(name, q4_0_linear_kernel<MR, 1, false, DOTS>, grid, dim3(kThreads), lds, stream, t);
 }
@@ -628,6 +743,8 @@ struct qxt_q4_0_batch {
     uint32_t chunk_count = 0;
     uint32_t grid = 0;
     int mr = 1;
+    int layout = 0;  // WeightLayout of every task (kEitherLayout when mixed)
+    int prefetch = 0;  // activation chunks per thread prefetched (every task one fp32 row), or 0
     size_t lds = 0;
 };
 
@@ -636,8 +753,22 @@ namespace {
 
 using BatchKernel = void (*)(const Q4Task *, const Q4Item *);
 
-BatchKernel batch_kernel(int mr) {
-    return mr == 1 ? q4_0_batch_kernel<1, units_per_thread(1)> : q4_0_batch_kernel<4, units_per_thread(4)>;
+template <int MR, int PC>
+BatchKernel batch_kernel_for(int layout) {
+    constexpr int U = PC > 0 ? kPrefetchUnits : units_per_thread(MR);
+    return layout == kLaneLayout    ? q4_0_batch_kernel<MR, U, kLaneLayout, PC>
+           : layout == kNativeRows ? q4_0_batch_kernel<MR, U, kNativeRows, PC>
+                                   : q4_0_batch_kernel<MR, U, kEitherLayout, PC>;
+}
+
+BatchKernel batch_kernel(int mr, int layout, int prefetch) {
+    if (mr != 1) return batch_kernel_for<4, 0>(layout);
+    switch (prefetch) {
+        case 2: return batch_kernel_for<1, 2>(layout);
+        case 4: return batch_kernel_for<1, 4>(layout);
+        case kMaxPrefetchChunks: return batch_kernel_for<1, kMaxPrefetchChunks>(layout);
+        default: return batch_kernel_for<1, 0>(layout);
+    }
 }
 
 }  // namespace
@@ -827,21 +958,62 @@ int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_
         max_rows = std::max(max_rows, d.rows);
     }
     const int mr = max_rows == 1 ? 1 : 4;
+    int layout = host[0].lanes ? kLaneLayout : kNativeRows;
+    for (uint32_t i = 1; i < count; ++i)
+        if ((host[i].lanes ? kLaneLayout : kNativeRows) != layout) layout = kEitherLayout;
+    // Tiles of one round of units each give a decode step's dependency stages
+    // (a few thousand columns) only 32-176 workgroups: most CUs idle while a
+    // few stream 70 KB each.  A batch whose tiles would not give every CU
+    // kBatchItemsPerCu workgroups narrows them until it does.
+    // Plans every task's tiles; returns the number of work items, or minus a
+    // status (with the error recorded).
+    auto plan_items = [&](int upt, int max_cpw, std::vector<Q4Item> *items, size_t *lds) -> int64_t {
+        uint64_t count_items = 0;
+        for (uint32_t i = 0; i < count; ++i) {
+            size_t task_lds = 0;
+            int rc = plan_task(host[i], mr, true, false, &task_lds, max_cpw, false, upt);
+            if (rc != QXT_OK) return -static_cast<int64_t>(rc);
+            if (lds != nullptr) *lds = std::max(*lds, task_lds);
+            count_items += (static_cast<uint64_t>(host[i].ncols) + host[i].cpw - 1) / host[i].cpw;
+            if (items != nullptr)
+                for (int c = 0; c < host[i].ncols; c += host[i].cpw)
+                    items->push_back({static_cast<int>(i), c, std::min(host[i].cpw, host[i].ncols - c)});
+        }
+        if (count_items > 0x7FFFFFFFu) return -static_cast<int64_t>(fail(QXT_INVALID_ARGUMENT, "q4_0 batch: too many work items"));
+        return static_cast<int64_t>(count_items);
+    };
+    uint64_t columns = 0;
+    for (uint32_t i = 0; i < count; ++i) columns += static_cast<uint64_t>(host[i].ncols);
+    const uint64_t want = static_cast<uint64_t>(kBatchItemsPerCu) * compute_units();
+    auto cap_for = [&](int64_t natural) {
+        return static_cast<uint64_t>(natural) < want ? static_cast<int>(std::max<uint64_t>(1, columns / want))
+                                                     : (1 << 30);
+    };
+    int64_t natural = plan_items(units_per_thread(mr), 1 << 30, nullptr, nullptr);
+    if (natural < 0) return static_cast<int>(-natural);
+    int max_cpw = cap_for(natural);
+    const int64_t planned = plan_items(units_per_thread(mr), max_cpw, nullptr, nullptr);
+    if (planned < 0) return static_cast<int>(-planned);
+    // Small batch: every workgroup quantises the rows it needs itself (an
+    // L2-resident re-read per workgroup) rather than waiting for a separate
+    // pre-pass launch.
+    const bool fused = static_cast<size_t>(planned) <= kFusedQuantItems;
+    // A small one-row batch whose every activation is an fp32 row of
+    // K <= 6144 runs the prefetch kernel, kPrefetchUnits units per thread:
+    // its tiles are planned for that.
+    bool prefetch_candidate = fused && mr == 1;
+    for (uint32_t i = 0; i < count && prefetch_candidate; ++i) prefetch_candidate = prefetch_chunks(host[i]) > 0;
+    const int upt = prefetch_candidate ? kPrefetchUnits : units_per_thread(mr);
+    if (upt != units_per_thread(mr)) {
+        natural = plan_items(upt, 1 << 30, nullptr, nullptr);
+        if (natural < 0) return static_cast<int>(-natural);
+        max_cpw = cap_for(natural);
+    }
     size_t lds = 0;
     std::vector<Q4Item> items;
-    for (uint32_t i = 0; i < count; ++i) {
-        size_t task_lds = 0;
-        int rc = plan_task(host[i], mr, true, false, &task_lds);
-        if (rc != QXT_OK) return rc;
-        lds = std::max(lds, task_lds);
-        for (int c = 0; c < host[i].ncols; c += host[i].cpw)
-            items.push_back({static_cast<int>(i), c, std::min(host[i].cpw, host[i].ncols - c)});
-    }
-    if (items.size() > 0x7FFFFFFFu) return fail(QXT_INVALID_ARGUMENT, "q4_0 batch: too many work items");
-    if (items.size() <= kFusedQuantItems) {
-        // Small batch: every workgroup quantises the rows it needs itself (an
-        // L2-resident re-read per workgroup) rather than waiting for a
-        // separate pre-pass launch.
+    const int64_t final_items = plan_items(upt, max_cpw, &items, &lds);
+    if (final_items < 0) return static_cast<int>(-final_items);
+    if (fused) {
         jobs.clear();
         job_task.clear();
     } else {
@@ -901,6 +1073,11 @@ int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_
     batch->chunk_count = static_cast<uint32_t>(chunks.size());
     batch->grid = static_cast<uint32_t>(items.size());
     batch->mr = mr;
+    batch->layout = layout;
+    // The prefetch kernel runs exactly the batches planned for it.
+    batch->prefetch = 0;
+    if (prefetch_candidate)
+        for (const Q4Task &t : host) batch->prefetch = std::max(batch->prefetch, prefetch_chunks(t));
     batch->lds = lds;
     *out = batch;
     return QXT_OK;
@@ -915,7 +1092,8 @@ int qxt_q4_0_batch_launch(const qxt_q4_0_batch *batch, void *stream) {
                     as_stream(stream), batch->jobs, batch->chunks);
         if (rc != QXT_OK) return rc;
     }
-    return launch("q4_0_batch_kernel", batch_kernel(batch->mr), dim3(batch->grid), dim3(kThreads), batch->lds,
+    return launch("q4_0_batch_kernel", batch_kernel(batch->mr, batch->layout, batch->prefetch), dim3(batch->grid), dim3(kThreads),
+                  batch->lds,
                   as_stream(stream), batch->tasks, batch->items);
 }
 

@@ -248,6 +248,8 @@ __device__ __forceinline__ float block_max(float v, float *scratch) {
     return v;
 }
 
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
 // NV > 0: the row (columns % 4 == 0, <= 1024 * NV columns) is held in registers.
 template <int NV, bool VEC>
 __global__ __launch_bounds__(kThreads) void rows_int8_kernel(const float *__restrict__ x, size_t x_stride,
@@ -261,12 +263,30 @@ __global__ __launch_bounds__(kThreads) void rows_int8_kernel(const float *__rest
     const uint32_t chunks = columns >> 2;
     float4 v[NV];
     float amax = 0.0f;
+    if constexpr (VEC) {
+        // The row is read once: non-temporal 16-byte loads, all issued before
+        // any is used (a lane past the row re-reads its last chunk, which
+        // leaves the maximum unchanged).  Measured on MI355X at 4096 rows:
+        // K = 14336 62 -> 49 us (4.7 -> 6.0 TB/s), K = 4096 19 -> 16 us,
+        // against loads guarded per lane.
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const uint32_t c = threadIdx.x + i * kThreads;
-        if (c < chunks) {
-            v[i] = load4<VEC>(src + 4 * c);
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t c = min(threadIdx.x + i * kThreads, chunks - 1);
+            const v4u raw = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(src) + c);
+            v[i] = make_float4(__uint_as_float(raw[0]), __uint_as_float(raw[1]), __uint_as_float(raw[2]),
+                               __uint_as_float(raw[3]));
+        }
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
             amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    } else {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t c = threadIdx.x + i * kThreads;
+            if (c < chunks) {
+                v[i] = load4<VEC>(src + 4 * c);
+                amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+            }
         }
     }
     const float s = row_scale(block_max(amax, scratch), floor);

@@ -463,3 +463,33 @@ def test_native_linear_at_k14336_small_rows_bit_exact(rows: int) -> None:
     wq, xq = oracle.quantize_q4_0_blocks(w), oracle.quantize_q8_0_blocks(x)
     out = q4.ggml_q4_0_q8_0_linear(dev(xq), dev(wq))
     np.testing.assert_array_equal(out.cpu().numpy(), oracle.q4_0_q8_0_reference(xq, wq))
+
+
+@pytest.mark.parametrize("shapes", [
+    # a decode step's dependency stages: q/k/v, o, gate/up, down (fp32 rows, K <= 6144)
+    [(1, 2048, 2048, 0, 2048), (1, 2048, 256, 0, 256), (1, 2048, 256, 0, 256)],
+    [(1, 2048, 5632, 0, 5632), (1, 2048, 5632, 0, 5632)],
+    [(1, 5632, 2048, 0, 2048)],
+    # K = 256 / 4096 / 6144 (two, four and six prefetched chunks per thread), ragged column ranges
+    [(1, 256, 48, 16, 17), (1, 256, 300, 5, 290)],
+    [(1, 4096, 1000, 8, 984), (1, 4096, 37, 0, 37)],
+    [(1, 6144, 700, 3, 650), (1, 2048, 64, 0, 64)],
+])
+def test_one_row_fp32_stage_batches_with_activation_prefetch_bit_exact(shapes) -> None:
+    # Small one-row batches whose activations are all fp32 rows: one launch,
+    # the row quantised in every workgroup after being requested before the
+    # weights; lane weights and native rows.
+    tasks, expected = _batch_case(41 + len(shapes), shapes, fused_every=1)
+    lane_tasks = [dict(t, weight=q4.pack_ggml_q4_0_lane_weights(t["weight"]),
+                       destination=torch.full_like(t["destination"], float(SENTINEL))) for t in tasks]
+    for batch_tasks in (tasks, lane_tasks):
+        with q4.Q4_0LinearBatch(batch_tasks) as batch:
+            assert batch.work_items <= 1024
+            for _ in range(2):
+                for t in batch_tasks:
+                    t["destination"][:, 16:] = -1.0
+                with _lib.launch_timing() as timing:
+                    batch.launch()
+                    torch.cuda.synchronize()
+                assert [name for name, _ in timing.records] == ["q4_0_batch_kernel"]
+                _check_batch(batch_tasks, expected)
