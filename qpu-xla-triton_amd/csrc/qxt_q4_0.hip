@@ -142,10 +142,9 @@ __device__ __forceinline__ void unit_block(const uint32_t (&d)[36], uint32_t &sb
     }
 }
 
-// Exact int32 dot of one Q4_0 block (packed nibbles qs) with one Q8_0 block.
-__device__ __forceinline__ int block_dot(const uint32_t (&qs)[4], const int *aq, int asum) {
-    const int4 a0 = *reinterpret_cast<const int4 *>(aq);
-    const int4 a1 = *reinterpret_cast<const int4 *>(aq + 4);
+// Exact int32 dot of one Q4_0 block (packed nibbles qs) with one Q8_0 block
+// (activation words a0, a1 and their element sum asum).
+__device__ __forceinline__ int block_dot(const uint32_t (&qs)[4], const int4 &a0, const int4 &a1, int asum) {
     int s = 0;
     s = dot4(static_cast<int>(qs[0] & 0x0F0F0F0Fu), a0.x, s);
     s = dot4(static_cast<int>(qs[1] & 0x0F0F0F0Fu), a0.y, s);
@@ -156,6 +155,10 @@ __device__ __forceinline__ int block_dot(const uint32_t (&qs)[4], const int *aq,
     s = dot4(static_cast<int>((qs[2] >> 4) & 0x0F0F0F0Fu), a1.z, s);
     s = dot4(static_cast<int>((qs[3] >> 4) & 0x0F0F0F0Fu), a1.w, s);
     return s - 8 * asum;
+}
+
+__device__ __forceinline__ int block_dot(const uint32_t (&qs)[4], const int *aq, int asum) {
+    return block_dot(qs, *reinterpret_cast<const int4 *>(aq), *reinterpret_cast<const int4 *>(aq + 4), asum);
 }
 
 // Quantise element chunk e (float4 v: elements 4 (e % 8) .. of block e / 8 of
@@ -428,6 +431,21 @@ __device__ __forceinline__ void compute_fast(const Q4Task &t, int col_base, int 
         const int g = u - col * G;
         float terms[MR][8];
         int idots[MR][8];
+        // One row: the unit's eight activation blocks are read from LDS up
+        // front (24 reads in flight, 80 registers) instead of one block at a
+        // time, which kept one or two reads in flight per unit.
+        int4 pre_lo[MR == 1 ? 8 : 1], pre_hi[MR == 1 ? 8 : 1];
+        int2 pre_ds[MR == 1 ? 8 : 1];
+        if constexpr (MR == 1) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int b = g * 8 + i;
+                pre_lo[i] = *reinterpret_cast<const int4 *>(aq + aq_index(b, 0));
+                pre_hi[i] = *reinterpret_cast<const int4 *>(aq + aq_index(b, 4));
+                pre_ds[i] = *reinterpret_cast<const int2 *>(ad + ad_index(b));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
         auto do_block = [&](auto ic) {
             constexpr int I = decltype(ic)::value;
             uint32_t sbits, qs[4];
@@ -436,8 +454,10 @@ __device__ __forceinline__ void compute_fast(const Q4Task &t, int col_base, int 
             const int b = g * 8 + I;
 #pragma unroll
             for (int r = 0; r < MR; ++r) {
-                const int2 ds = *reinterpret_cast<const int2 *>(ad + r * geo.ad_row + ad_index(b));
-                const int dot = block_dot(qs, aq + r * geo.aq_row + aq_index(b, 0), ds.y);
+                const int2 ds = MR == 1 ? pre_ds[I % (MR == 1 ? 8 : 1)]
+                                        : *reinterpret_cast<const int2 *>(ad + r * geo.ad_row + ad_index(b));
+                const int dot = MR == 1 ? block_dot(qs, pre_lo[I % (MR == 1 ? 8 : 1)], pre_hi[I % (MR == 1 ? 8 : 1)], ds.y)
+                                        : block_dot(qs, aq + r * geo.aq_row + aq_index(b, 0), ds.y);
                 idots[r][I] = dot;
                 float v = static_cast<float>(dot) * dw;
                 v = v * __int_as_float(ds.x);
@@ -618,6 +638,14 @@ constexpr int units_per_thread(int mr) { return mr == 1 ? 2 : 1; }
 #define QXT_PREFETCH_UNITS 1
 #endif
 constexpr int kPrefetchUnits = QXT_PREFETCH_UNITS;
+
+// Whether one-row fp32 batches too large for the fused path (a whole decode
+// step) still quantise inside each workgroup, with the activation prefetch,
+// instead of running a pre-pass launch.
+#ifndef QXT_PREFETCH_LARGE
+#define QXT_PREFETCH_LARGE 0
+#endif
+constexpr bool kPrefetchLargeBatches = QXT_PREFETCH_LARGE != 0;
 static_assert(kPrefetchUnits >= 1 && kPrefetchUnits <= units_per_thread(1),
               "a prefetch plan must fit the one-row batch kernel it falls back to");
 
@@ -745,6 +773,7 @@ struct qxt_q4_0_batch {
     int mr = 1;
     int layout = 0;  // WeightLayout of every task (kEitherLayout when mixed)
     int prefetch = 0;  // activation chunks per thread prefetched (every task one fp32 row), or 0
+    int upt = 1;       // units per thread of the batch kernel
     size_t lds = 0;
 };
 
@@ -753,22 +782,28 @@ namespace {
 
 using BatchKernel = void (*)(const Q4Task *, const Q4Item *);
 
-template <int MR, int PC>
+template <int MR, int U, int PC>
 BatchKernel batch_kernel_for(int layout) {
-    constexpr int U = PC > 0 ? kPrefetchUnits : units_per_thread(MR);
     return layout == kLaneLayout    ? q4_0_batch_kernel<MR, U, kLaneLayout, PC>
            : layout == kNativeRows ? q4_0_batch_kernel<MR, U, kNativeRows, PC>
                                    : q4_0_batch_kernel<MR, U, kEitherLayout, PC>;
 }
 
-BatchKernel batch_kernel(int mr, int layout, int prefetch) {
-    if (mr != 1) return batch_kernel_for<4, 0>(layout);
+template <int U>
+BatchKernel prefetch_kernel(int layout, int prefetch) {
     switch (prefetch) {
-        case 2: return batch_kernel_for<1, 2>(layout);
-        case 4: return batch_kernel_for<1, 4>(layout);
-        case kMaxPrefetchChunks: return batch_kernel_for<1, kMaxPrefetchChunks>(layout);
-        default: return batch_kernel_for<1, 0>(layout);
+        case 2: return batch_kernel_for<1, U, 2>(layout);
+        case 4: return batch_kernel_for<1, U, 4>(layout);
+        default: return batch_kernel_for<1, U, kMaxPrefetchChunks>(layout);
     }
+}
+
+// The kernel of a batch: rows per task group, weight layout, activation
+// chunks prefetched per thread (0: none) and units per thread.
+BatchKernel batch_kernel(int mr, int layout, int prefetch, int upt) {
+    if (mr != 1) return batch_kernel_for<4, units_per_thread(4), 0>(layout);
+    if (prefetch == 0) return batch_kernel_for<1, units_per_thread(1), 0>(layout);
+    return upt == 1 ? prefetch_kernel<1>(layout, prefetch) : prefetch_kernel<units_per_thread(1)>(layout, prefetch);
 }
 
 }  // namespace
@@ -994,16 +1029,21 @@ int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_
     int max_cpw = cap_for(natural);
     const int64_t planned = plan_items(units_per_thread(mr), max_cpw, nullptr, nullptr);
     if (planned < 0) return static_cast<int>(-planned);
-    // Small batch: every workgroup quantises the rows it needs itself (an
-    // L2-resident re-read per workgroup) rather than waiting for a separate
-    // pre-pass launch.
-    const bool fused = static_cast<size_t>(planned) <= kFusedQuantItems;
-    // A small one-row batch whose every activation is an fp32 row of
-    // K <= 6144 runs the prefetch kernel, kPrefetchUnits units per thread:
-    // its tiles are planned for that.
-    bool prefetch_candidate = fused && mr == 1;
+    // A one-row batch whose every activation is an fp32 row of K <= 6144
+    // can run the prefetch kernel: each workgroup requests its row before
+    // its weights and quantises it while they are in flight.  A batch whose
+    // tiles were narrowed (too few columns to fill the chip) runs it with
+    // kPrefetchUnits units per thread, its tiles planned for that.
+    bool prefetch_candidate = mr == 1;
     for (uint32_t i = 0; i < count && prefetch_candidate; ++i) prefetch_candidate = prefetch_chunks(host[i]) > 0;
-    const int upt = prefetch_candidate ? kPrefetchUnits : units_per_thread(mr);
+    const bool small = static_cast<size_t>(planned) <= kFusedQuantItems;
+    if (!small && !kPrefetchLargeBatches) prefetch_candidate = false;
+    // Every other small batch quantises its fp32 rows inside each workgroup
+    // too (an L2-resident re-read per workgroup) rather than waiting for a
+    // separate pre-pass launch; larger ones run the pre-pass.
+    const bool fused = small || prefetch_candidate;
+    const bool narrowed = max_cpw < (1 << 30);
+    const int upt = prefetch_candidate && narrowed ? kPrefetchUnits : units_per_thread(mr);
     if (upt != units_per_thread(mr)) {
         natural = plan_items(upt, 1 << 30, nullptr, nullptr);
         if (natural < 0) return static_cast<int>(-natural);
@@ -1076,6 +1116,7 @@ int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_
     batch->layout = layout;
     // The prefetch kernel runs exactly the batches planned for it.
     batch->prefetch = 0;
+    batch->upt = upt;
     if (prefetch_candidate)
         for (const Q4Task &t : host) batch->prefetch = std::max(batch->prefetch, prefetch_chunks(t));
     batch->lds = lds;
@@ -1092,7 +1133,7 @@ int qxt_q4_0_batch_launch(const qxt_q4_0_batch *batch, void *stream) {
                     as_stream(stream), batch->jobs, batch->chunks);
         if (rc != QXT_OK) return rc;
     }
-    return launch("q4_0_batch_kernel", batch_kernel(batch->mr, batch->layout, batch->prefetch), dim3(batch->grid), dim3(kThreads),
+    return launch("q4_0_batch_kernel", batch_kernel(batch->mr, batch->layout, batch->prefetch, batch->upt), dim3(batch->grid), dim3(kThreads),
                   batch->lds,
                   as_stream(stream), batch->tasks, batch->items);
 }
