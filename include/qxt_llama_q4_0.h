@@ -28,8 +28,12 @@
  *    the reference links and keeps its control flow) but computes nothing:
  *    the library has no CPU compute path, so it returns
  *    QXT_CAPABILITY_MISSING and leaves the destination untouched;
- *  - only QXT_LLAMA_Q4_0_WEIGHT_EXACT is provided; the reference's approximate
- *    COLUMN_W8 / ROWCOL_W8A8 modes return QXT_CAPABILITY_MISSING.
+ *  - the approximate COLUMN_W8 / ROWCOL_W8A8 modes (rows > 4, as in the
+ *    reference) re-quantise the weights on the GPU at prepare time and run on
+ *    the int8 matrix cores: COLUMN_W8 on the split-plane Q4_0 prefill kernel
+ *    with one fp32 scale per column, ROWCOL_W8A8 on the W8A8 GEMM after a
+ *    per-row int8 re-quantisation of each submitted activation; they need
+ *    rows * K and resident columns * K below 2^31 (else QXT_CAPABILITY_MISSING).
  */
 #ifndef QXT_LLAMA_Q4_0_H
 #define QXT_LLAMA_Q4_0_H
@@ -62,8 +66,12 @@ typedef struct qxt_llama_context_config {
 /* Replaces qpu_llama_q4_0_weight_mode (qpu_llama_q4_0.h:16-20). */
 typedef enum qxt_llama_q4_0_weight_mode {
     QXT_LLAMA_Q4_0_WEIGHT_EXACT = 0,
-    QXT_LLAMA_Q4_0_WEIGHT_COLUMN_W8 = 1,  /* not provided: QXT_CAPABILITY_MISSING */
-    QXT_LLAMA_Q4_0_WEIGHT_ROWCOL_W8A8 = 2 /* not provided: QXT_CAPABILITY_MISSING */
+    /* int8 weights, one fp32 scale per column (qpu_llama_q4_0.c:332-386):
+     * y = fl32(sum_b fl32(float(dot_b) * da_b) * cs[n]), block order. */
+    QXT_LLAMA_Q4_0_WEIGHT_COLUMN_W8 = 1,
+    /* int8 weights and int8 activation rows, one fp32 scale each
+     * (qpu_llama_q4_0.c:526-571, 899-906): y = fl32(fl32(float(dot) * rs[m]) * cs[n]). */
+    QXT_LLAMA_Q4_0_WEIGHT_ROWCOL_W8A8 = 2
 } qxt_llama_q4_0_weight_mode;
 
 /* Host layout of desc.weights. */

@@ -49,6 +49,13 @@ Pinning status (what each function is checked against, in ``tests/``):
   gelu is the identity or exactly zero); dequantised blocks within half a
   step of gelu(gate) * up computed in float64; the split planes against the
   native blocks byte for byte.
+* ``oracle/llama_approx.py`` (the bridge's COLUMN_W8 / ROWCOL_W8A8 modes):
+  hand-worked columns and rows whose literal codes separate half-away
+  rounding from half-even and exact rounding (the fp32 ``+ 0.5`` before the
+  truncation), zero columns and rows, random data re-derived in exact
+  rational arithmetic (on data where a reciprocal multiply would differ),
+  power-of-two-scale linears that are exact, and a case where applying the
+  column scale per block rounds differently from applying it once.
 * ``quantize_q4_0_blocks``: ggml's published ``quantize_row_q4_0_ref`` rule
   (upstream ggml is not vendored in the reference, so there is no runnable
   copy); pinned by hand-worked known-answer blocks whose literal codes and

@@ -68,6 +68,23 @@ int q4_0_tiled_native(const void *activation, size_t activation_row_stride, cons
 // message (qxt_q4_0.hip).
 int q4_0_linear_capability(uint32_t rows, uint32_t blocks);
 
+// Operands of the llama.cpp bridge's approximate weight modes
+// (qxt_llama_approx.hip).  Weight codes are uint32 words of four consecutive
+// k: word (i, n) at weight_q + i * weight_q_row_stride bytes + 4 n, i < blocks * 8;
+// activation codes int8 [rows, blocks * 32] contiguous.
+int q4_0_columns_w8(const void *weight, size_t weight_row_stride, uint32_t columns, uint32_t blocks,
+                    uint32_t *weight_q, size_t weight_q_row_stride, float *column_scales, hipStream_t stream);
+int q8_0_rows_w8(const void *activation, size_t activation_row_stride, uint32_t rows, uint32_t blocks,
+                 int8_t *activation_q, float *row_scales, hipStream_t stream);
+int q8_0_split_planes(const void *activation, size_t activation_row_stride, uint32_t rows, uint32_t blocks,
+                      int8_t *activation_q, uint16_t *activation_scales, hipStream_t stream);
+// COLUMN_W8 linear on the int8 matrix cores (qxt_q4_0_tiled.hip): split
+// activation planes, weight codes as above, fp32 column scales.
+int q4_0_tiled_column_w8(const int8_t *activation_q, const uint16_t *activation_scales, const uint32_t *weight_q,
+                         size_t weight_q_row_stride, const float *column_scales, float *destination,
+                         size_t destination_row_stride, uint32_t rows, uint32_t blocks, uint32_t columns,
+                         hipStream_t stream);
+
 // -------------------------------------------------------------- device side
 
 constexpr int QK = 32;            // elements per GGML block

@@ -173,7 +173,13 @@ struct qxt_llama_q4_0_linear {
     size_t resident_bytes = 0;
     size_t weight_bytes = 0;
     bool lanes = false;               // weight in the lane layout (decode-sized linears)
-    void *weight = nullptr;           // device Q4_0 [resident_count][blocks] (native or lane layout)
+    qxt_llama_q4_0_weight_mode mode = QXT_LLAMA_Q4_0_WEIGHT_EXACT;
+    // EXACT: device Q4_0 [resident_count][blocks] (native or lane layout).
+    // COLUMN_W8 / ROWCOL_W8A8: int8 codes as uint32 words [blocks * 8][resident_count].
+    void *weight = nullptr;
+    float *column_scales = nullptr;   // approximate modes: fp32 [resident_count]
+    int8_t *activation_q = nullptr;   // approximate modes: int8 [rows][blocks * 32]
+    void *activation_scales = nullptr;  // COLUMN_W8: fp16 bits [rows][blocks]; ROWCOL_W8A8: fp32 [rows]
     void *activation = nullptr;       // device Q8_0 [rows][blocks]
     void *activation_packed = nullptr;  // device copy of interleaved host rows
     float *output = nullptr;          // device fp32 [rows][resident_count]
@@ -204,13 +210,15 @@ namespace {
 
 void release_buffers(qxt_llama_q4_0_linear *l) {
     if (l->done) (void)hipEventDestroy(l->done);
-    for (void *p : {l->weight, l->activation, l->activation_packed, static_cast<void *>(l->output)})
+    for (void *p : {l->weight, l->activation, l->activation_packed, static_cast<void *>(l->output),
+                    static_cast<void *>(l->column_scales), static_cast<void *>(l->activation_q), l->activation_scales})
         if (p) (void)hipFree(p);
     if (l->host_activation) (void)hipHostFree(l->host_activation);
     if (l->host_output) (void)hipHostFree(l->host_output);
     l->done = nullptr;
-    l->weight = l->activation = l->activation_packed = nullptr;
-    l->output = nullptr;
+    l->weight = l->activation = l->activation_packed = l->activation_scales = nullptr;
+    l->output = l->column_scales = nullptr;
+    l->activation_q = nullptr;
     l->host_activation = nullptr;
     l->host_output = nullptr;
 }
@@ -228,7 +236,9 @@ void end_submission(qxt_llama_q4_0_linear *l, bool poison) {
 
 // Copy the resident weight columns to the device, unpacking CPU_REPACK groups
 // and, for decode-sized linears, re-laying the native rows out in the lane
-// layout the decode kernels stream fastest (qxt_q4_0_pack_lanes).
+// layout the decode kernels stream fastest (qxt_q4_0_pack_lanes); in the
+// approximate modes, re-quantising each column to int8 codes with one fp32
+// scale (qpu_llama_q4_0.c:332-386).
 int upload_weights(qxt_llama_q4_0_linear *l, const qxt_llama_q4_0_linear_desc *d) {
     qxt_llama_context *ctx = l->context;
     const size_t bytes = static_cast<size_t>(l->resident_count) * l->weight_row_bytes;
@@ -236,16 +246,17 @@ int upload_weights(qxt_llama_q4_0_linear *l, const qxt_llama_q4_0_linear_desc *d
     // layouts (a CPU_REPACK group of 4 columns is 4 native rows long, start % 4 == 0).
     const uint8_t *src = static_cast<const uint8_t *>(d->weights) + l->resident_start * l->weight_row_bytes;
     const bool repack = d->weight_format == QXT_LLAMA_Q4_0_FORMAT_REPACK_4X4;
+    const bool approximate = l->mode != QXT_LLAMA_Q4_0_WEIGHT_EXACT;
     void *raw = nullptr;     // host bytes as uploaded, when they are not yet native rows
     void *native = nullptr;  // native rows, when they are not the final layout
     hipError_t err = hipSuccess;
     if (repack) err = hipMalloc(&raw, bytes);
-    if (err == hipSuccess && l->lanes) err = hipMalloc(&native, bytes);
+    if (err == hipSuccess && (l->lanes || approximate)) err = hipMalloc(&native, bytes);
     if (err != hipSuccess) {
         (void)hipFree(raw);
         return ctx->fail(QXT_ALLOCATION_FAILED, "weight staging: %s", hipGetErrorString(err));
     }
-    void *rows = l->lanes ? native : l->weight;
+    void *rows = l->lanes || approximate ? native : l->weight;
     err = hipMemcpyAsync(repack ? raw : rows, src, bytes, hipMemcpyHostToDevice, ctx->stream);
     if (err == hipSuccess && repack) {
         const size_t items = static_cast<size_t>(l->resident_count) * l->blocks;
@@ -259,6 +270,12 @@ int upload_weights(qxt_llama_q4_0_linear *l, const qxt_llama_q4_0_linear_desc *d
         rc = qxt_q4_0_pack_lanes(native, l->weight_row_bytes, l->weight, l->weight_bytes, l->resident_count, l->blocks,
                                  ctx->stream);
         if (rc != QXT_OK) rc = ctx->fail(rc, "weight re-layout: %s", qxt_last_error());
+    }
+    if (err == hipSuccess && approximate) {
+        rc = qxt::q4_0_columns_w8(native, l->weight_row_bytes, l->resident_count, l->blocks,
+                                  static_cast<uint32_t *>(l->weight), static_cast<size_t>(l->resident_count) * 4,
+                                  l->column_scales, ctx->stream);
+        if (rc != QXT_OK) rc = ctx->fail(rc, "weight re-quantisation: %s", qxt_last_error());
     }
     const hipError_t sync = hipStreamSynchronize(ctx->stream);
     (void)hipFree(raw);
@@ -357,12 +374,21 @@ extern "C" int qxt_llama_q4_0_linear_prepare(qxt_llama_context *context, const q
         !mul_size(d->resident_column_count, sizeof(float), &out_row) || !mul_size(d->rows, out_row, &out_bytes)) {
         return context->fail(QXT_INVALID_ARGUMENT, "q4_0 prepare: weight size or extents do not fit");
     }
-    if (d->weight_mode != QXT_LLAMA_Q4_0_WEIGHT_EXACT)
-        return context->fail(QXT_CAPABILITY_MISSING, "q4_0 prepare: only the exact weight mode is provided");
-    // Every submission (any row count up to d->rows) must be runnable: reject
-    // a K whose activation rows do not fit a workgroup's LDS now, not at submit.
-    if (qxt::q4_0_linear_capability(d->rows, static_cast<uint32_t>(blocks)) != QXT_OK)
+    const bool approximate = d->weight_mode != QXT_LLAMA_Q4_0_WEIGHT_EXACT;
+    if (approximate) {
+        // The approximate modes run on the split-plane matrix-core kernel or
+        // the W8A8 GEMM: 32-bit buffer offsets bound every operand.
+        const uint64_t k = static_cast<uint64_t>(blocks) * qxt::QK;
+        if (static_cast<uint64_t>(d->rows) * k >= (1ull << 31) ||
+            static_cast<uint64_t>(d->resident_column_count) * k >= (1ull << 31) ||
+            (d->weight_mode == QXT_LLAMA_Q4_0_WEIGHT_ROWCOL_W8A8 && k * 127 * 127 > 2147483647ull))
+            return context->fail(QXT_CAPABILITY_MISSING,
+                                 "q4_0 prepare: approximate weight modes need rows * K and columns * K below 2^31");
+    } else if (qxt::q4_0_linear_capability(d->rows, static_cast<uint32_t>(blocks)) != QXT_OK) {
+        // Every submission (any row count up to d->rows) must be runnable: reject
+        // a K whose activation rows do not fit a workgroup's LDS now, not at submit.
         return context->fail(QXT_CAPABILITY_MISSING, "q4_0 prepare: %s", qxt_last_error());
+    }
     if (context->injected(QXT_FAIL_SOURCE_HASH)) return context->fail(QXT_HASH_MISMATCH, "injected source hash mismatch");
     if (std::strcmp(d->expected_source_hash, QXT_Q4_0_SOURCE_HASH) != 0)
         return context->fail(QXT_HASH_MISMATCH, "expected source hash %.64s does not match this build (%s)",
@@ -381,17 +407,32 @@ extern "C" int qxt_llama_q4_0_linear_prepare(qxt_llama_context *context, const q
     l->weight_row_bytes = weight_row_bytes;
     l->activation_row_bytes = act_row;
     l->output_row_bytes = out_row;
+    l->mode = d->weight_mode;
     // Linears of fewer than 16 rows run on the v_dot4 decode kernel, which
     // streams the lane layout fastest; prefill-sized ones on the matrix cores
     // over native rows.
-    l->lanes = d->rows < 16 && blocks % 8 == 0;
-    l->weight_bytes = l->lanes ? qxt_q4_0_lanes_bytes(d->resident_column_count, static_cast<uint32_t>(blocks))
-                               : resident_weight;
+    l->lanes = !approximate && d->rows < 16 && blocks % 8 == 0;
+    const size_t k = blocks * qxt::QK;
+    const size_t approx_scales = d->weight_mode == QXT_LLAMA_Q4_0_WEIGHT_ROWCOL_W8A8 ? sizeof(float)
+                                                                                     : blocks * sizeof(uint16_t);
+    l->weight_bytes = approximate ? static_cast<size_t>(d->resident_column_count) * k
+                      : l->lanes ? qxt_q4_0_lanes_bytes(d->resident_column_count, static_cast<uint32_t>(blocks))
+                                 : resident_weight;
     // Device: weight, activation (+ its interleaved landing copy), output; pinned: activation, output.
     l->resident_bytes = l->weight_bytes + 2 * act_bytes + out_bytes + act_bytes + out_bytes;
+    // Approximate modes: column scales, activation codes and their scales.
+    if (approximate)
+        l->resident_bytes += static_cast<size_t>(d->resident_column_count) * sizeof(float) +
+                             static_cast<size_t>(d->rows) * (k + approx_scales);
 
     DeviceScope scope(context->device);
     hipError_t err = hipMalloc(&l->weight, l->weight_bytes);
+    if (err == hipSuccess && approximate) {
+        err = hipMalloc(reinterpret_cast<void **>(&l->column_scales),
+                        static_cast<size_t>(d->resident_column_count) * sizeof(float));
+        if (err == hipSuccess) err = hipMalloc(reinterpret_cast<void **>(&l->activation_q), static_cast<size_t>(d->rows) * k);
+        if (err == hipSuccess) err = hipMalloc(&l->activation_scales, static_cast<size_t>(d->rows) * approx_scales);
+    }
     if (err == hipSuccess) err = hipMalloc(&l->activation, act_bytes);
     if (err == hipSuccess) err = hipMalloc(&l->activation_packed, act_bytes);
     if (err == hipSuccess) err = hipMalloc(reinterpret_cast<void **>(&l->output), out_bytes);
@@ -493,7 +534,32 @@ extern "C" int qxt_llama_q4_0_linear_submit(qxt_llama_q4_0_linear *l, const qxt_
     s->input_copy_end = now_ns();
     s->submit_start = s->input_copy_end;
     int rc = QXT_OK;
-    if (err == hipSuccess) {
+    if (err == hipSuccess && l->mode == QXT_LLAMA_Q4_0_WEIGHT_COLUMN_W8) {
+        // Split planes of the Q8_0 rows, then the column-scale tiled linear
+        // (qpu_llama_q4_0.c:572-607, 669-684).
+        uint16_t *scales = static_cast<uint16_t *>(l->activation_scales);
+        rc = qxt::q8_0_split_planes(l->activation, l->activation_row_bytes, rows, l->blocks, l->activation_q, scales,
+                                    ctx->stream);
+        if (rc == QXT_OK)
+            rc = qxt::q4_0_tiled_column_w8(l->activation_q, scales, static_cast<const uint32_t *>(l->weight) + local,
+                                           static_cast<size_t>(l->resident_count) * 4, l->column_scales + local,
+                                           l->output + local, l->output_row_bytes, rows, l->blocks, e->column_count,
+                                           ctx->stream);
+        if (rc != QXT_OK) rc = ctx->fail(QXT_SUBMISSION_FAILED, "q4_0 column-w8 linear: %s", qxt_last_error());
+    } else if (err == hipSuccess && l->mode == QXT_LLAMA_Q4_0_WEIGHT_ROWCOL_W8A8) {
+        // Per-row int8 re-quantisation of the Q8_0 rows, then the W8A8 GEMM
+        // with the row x column scale epilogue (qpu_llama_q4_0.c:526-571, 654-668).
+        const uint32_t k = l->blocks * qxt::QK;
+        float *row_scales = static_cast<float *>(l->activation_scales);
+        rc = qxt::q8_0_rows_w8(l->activation, l->activation_row_bytes, rows, l->blocks, l->activation_q, row_scales,
+                               ctx->stream);
+        if (rc == QXT_OK)
+            rc = qxt_w8a8_gemm_dequantize(l->activation_q, k, static_cast<const uint32_t *>(l->weight) + local,
+                                          static_cast<size_t>(l->resident_count) * 4, row_scales,
+                                          l->column_scales + local, nullptr, l->output + local, l->output_row_bytes,
+                                          rows, e->column_count, k, QXT_W8A8_WEIGHT_K4N, ctx->stream);
+        if (rc != QXT_OK) rc = ctx->fail(QXT_SUBMISSION_FAILED, "q4_0 rowcol-w8a8 linear: %s", qxt_last_error());
+    } else if (err == hipSuccess) {
         rc = l->lanes ? qxt_ggml_q4_0_q8_0_linear_lanes(l->activation, l->activation_row_bytes, l->weight,
                                                         l->resident_count, l->output, l->output_row_bytes, rows,
                                                         l->blocks, local, local, e->column_count, ctx->stream)

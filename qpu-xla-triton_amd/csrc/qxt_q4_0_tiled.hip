@@ -52,6 +52,7 @@ struct TiledArgs {
     const uint8_t *as;   // fp16 scales [M, B] as 2- or 4-byte elements
     const uint8_t *wq;   // uint32 [B * 8, N]
     const uint8_t *ws;   // fp16 scales [B, N]
+    const float *cs;     // fp32 column scales [N] (column-scale variant, ws unused)
     // native layout
     const uint8_t *act;  // Q8_0 [M, B, 34]
     const uint8_t *w;    // Q4_0 [>= wcol0 + N, B, 18]
@@ -108,6 +109,11 @@ __device__ __forceinline__ void frags_of(const RawFrags &f, v4i &a, v4i &w) {
 constexpr int kAhead = 4;  // blocks of fragments in flight ahead of the one being reduced
 static_assert(kAhead % 2 == 0 && kChunk % kAhead == 0, "block parity must be static in the unrolled loop");
 
+// COLUMN: the column-scale variant (the llama.cpp bridge's COLUMN_W8 weight
+// mode): int8 weights with one fp32 scale per column instead of fp16 block
+// scales; each block adds fl32(float(dot) * da) and the column scale
+// multiplies the finished sum once (ggml_q4_0.py:497-525).
+template <bool COLUMN>
 __global__ __launch_bounds__(kThreads) void q4_0_tiled_kernel(TiledArgs t) {
     // Scales of two chunks: the one being reduced and the next, written
     // while the current one is reduced (one barrier per chunk).
@@ -164,7 +170,7 @@ __global__ __launch_bounds__(kThreads) void q4_0_tiled_kernel(TiledArgs t) {
             const uint32_t ao = in_k && m < t.m ? static_cast<uint32_t>(m) * t.as_stride + b * t.as_bytes : kOutOfRange;
             const uint32_t wo = in_k && n < t.n ? static_cast<uint32_t>(b) * t.ws_stride + n * 2 : kOutOfRange;
             da_bits[u] = __builtin_amdgcn_raw_buffer_load_b16(ras, ao, 0, 0);
-            dw_bits[u] = __builtin_amdgcn_raw_buffer_load_b16(rws, wo, 0, 0);
+            if constexpr (!COLUMN) dw_bits[u] = __builtin_amdgcn_raw_buffer_load_b16(rws, wo, 0, 0);
         }
     };
     auto store_scales = [&](int buf) {
@@ -173,7 +179,7 @@ __global__ __launch_bounds__(kThreads) void q4_0_tiled_kernel(TiledArgs t) {
             const int i = threadIdx.x + u * kThreads;
             const int cb = i / kTile, r = i - cb * kTile;
             s_da[buf][cb][r] = half_bits_to_float(da_bits[u]);
-            s_dw[buf][cb][r] = half_bits_to_float(dw_bits[u]);
+            if constexpr (!COLUMN) s_dw[buf][cb][r] = half_bits_to_float(dw_bits[u]);
         }
     };
     load_scales(0);
@@ -195,7 +201,7 @@ __global__ __launch_bounds__(kThreads) void q4_0_tiled_kernel(TiledArgs t) {
             float4 gda[kAhead][4];
 #pragma unroll
             for (int j = 0; j < kAhead; ++j) {
-                gdw[j] = s_dw[buf][cb0 + j][wn * 32 + l32];
+                if constexpr (!COLUMN) gdw[j] = s_dw[buf][cb0 + j][wn * 32 + l32];
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
                     gda[j][q] = *reinterpret_cast<const float4 *>(&s_da[buf][cb0 + j][wm * 32 + 8 * q + 4 * h]);
@@ -213,13 +219,14 @@ __global__ __launch_bounds__(kThreads) void q4_0_tiled_kernel(TiledArgs t) {
                     issue_frags(t, ra, rw, base, c0 + cb + 1 + kAhead, ring[jn]);
                 }
                 const v16i &d = dots[j & 1];
-                const float dw = gdw[j];
+                const float dw = COLUMN ? 1.0f : gdw[j];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const float das[4] = {gda[j][q].x, gda[j][q].y, gda[j][q].z, gda[j][q].w};
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        float v = static_cast<float>(d[4 * q + e]) * dw;
+                        float v = static_cast<float>(d[4 * q + e]);
+                        if constexpr (!COLUMN) v = v * dw;
                         v = v * das[e];
                         acc[4 * q + e] = acc[4 * q + e] + v;
                     }
@@ -233,6 +240,7 @@ __global__ __launch_bounds__(kThreads) void q4_0_tiled_kernel(TiledArgs t) {
         __syncthreads();
     }
     if (!b_ok) return;
+    const float cs = COLUMN ? t.cs[bn] : 1.0f;
 #pragma unroll
     for (int q = 0; q < 4; ++q)
 #pragma unroll
@@ -240,7 +248,7 @@ __global__ __launch_bounds__(kThreads) void q4_0_tiled_kernel(TiledArgs t) {
             const int m = m0 + wm * 32 + 8 * q + 4 * h + e;
             if (m < t.m)
                 reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(t.y) + static_cast<size_t>(m) * t.y_stride)[t.ocol0 + bn] =
-                    acc[4 * q + e];
+                    COLUMN ? acc[4 * q + e] * cs : acc[4 * q + e];
         }
 }
 
@@ -467,7 +475,8 @@ int launch_tiled(const TiledArgs &t, bool native, hipStream_t stream) {
     // planes are read as fragments directly (measured on MI355X at M = 512:
     // native gate_up 103 -> 42 us staged; split 44 us direct, 64 us staged).
     if (native) return launch("q4_0_tiled_kernel", q4_0_staged_kernel, grid, dim3(kThreads), 0, stream, t);
-    return launch("q4_0_tiled_kernel", q4_0_tiled_kernel, grid, dim3(kThreads), 0, stream, t);
+    if (t.cs != nullptr) return launch("q4_0_tiled_kernel", q4_0_tiled_kernel<true>, grid, dim3(kThreads), 0, stream, t);
+    return launch("q4_0_tiled_kernel", q4_0_tiled_kernel<false>, grid, dim3(kThreads), 0, stream, t);
 }
 
 bool below_2gib(uint64_t bytes) { return bytes < (1ull << 31); }
@@ -502,6 +511,36 @@ int q4_0_tiled_native(const void *activation, size_t activation_row_stride, cons
     t.wcol0 = static_cast<int>(weight_column_start);
     t.ocol0 = static_cast<int>(output_column_start);
     return launch_tiled(t, true, stream);
+}
+
+int q4_0_tiled_column_w8(const int8_t *activation_q, const uint16_t *activation_scales, const uint32_t *weight_q,
+                         size_t weight_q_row_stride, const float *column_scales, float *destination,
+                         size_t destination_row_stride, uint32_t rows, uint32_t blocks, uint32_t columns,
+                         hipStream_t stream) {
+    const uint64_t k = static_cast<uint64_t>(blocks) * 32;
+    const uint64_t a_extent = static_cast<uint64_t>(rows) * k;
+    const uint64_t as_extent = static_cast<uint64_t>(rows) * blocks * 2;
+    const uint64_t w_extent = static_cast<uint64_t>(blocks * 8ull - 1) * weight_q_row_stride + columns * 4ull;
+    if (!below_2gib(a_extent) || !below_2gib(as_extent) || !below_2gib(w_extent))
+        return fail(QXT_INVALID_ARGUMENT, "q4_0 column-w8 linear: operands must be smaller than 2 GiB");
+    TiledArgs t{};
+    t.aq = reinterpret_cast<const uint8_t *>(activation_q);
+    t.as = reinterpret_cast<const uint8_t *>(activation_scales);
+    t.wq = reinterpret_cast<const uint8_t *>(weight_q);
+    t.cs = column_scales;
+    t.y = destination;
+    t.aq_stride = static_cast<uint32_t>(k);
+    t.as_stride = blocks * 2;
+    t.as_bytes = 2;
+    t.wq_stride = static_cast<uint32_t>(weight_q_row_stride);
+    t.y_stride = destination_row_stride;
+    t.a_extent = static_cast<uint32_t>(a_extent);
+    t.as_extent = static_cast<uint32_t>(as_extent);
+    t.w_extent = static_cast<uint32_t>(w_extent);
+    t.m = static_cast<int>(rows);
+    t.n = static_cast<int>(columns);
+    t.blocks = static_cast<int>(blocks);
+    return launch_tiled(t, false, stream);
 }
 
 }  // namespace qxt

@@ -19,6 +19,7 @@ from conftest import load_golden
 from qpu_xla_amd import _lib
 from qpu_xla_amd.llama_bridge import (
     FORMAT_REPACK_4X4,
+    WEIGHT_COLUMN_W8,
     WEIGHT_ROWCOL_W8A8,
     Execution,
     LlamaContext,
@@ -127,11 +128,11 @@ def test_native_safety_matrix(rows: int) -> None:
         status, handle = LlamaQ4_0Linear.prepare_status(ctx, weights[GUARD:GUARD + w_bytes],
                                                         weight_size=w_bytes - 1, **_desc(weights, **base))
         assert status == _lib.INVALID_ARGUMENT and not handle.value
-        # The reference's approximate weight modes are not provided.
-        status, handle = LlamaQ4_0Linear.prepare_status(ctx, weights[GUARD:GUARD + w_bytes],
-                                                        weight_mode=WEIGHT_ROWCOL_W8A8,
-                                                        **_desc(weights, k=k, n=n, rows=16))
-        assert status == _lib.CAPABILITY_MISSING and not handle.value
+        # The approximate weight modes need more than four rows (qpu_llama_q4_0.c:219).
+        for mode in (WEIGHT_COLUMN_W8, WEIGHT_ROWCOL_W8A8):
+            status, handle = LlamaQ4_0Linear.prepare_status(ctx, weights[GUARD:GUARD + w_bytes], weight_mode=mode,
+                                                            **_desc(weights, k=k, n=n, rows=4))
+            assert status == _lib.INVALID_ARGUMENT and not handle.value
 
         with LlamaQ4_0Linear(ctx, weights[GUARD:GUARD + w_bytes], **_desc(weights, **base)) as linear:
             def run(start: int, count: int, *, a_size: int = GUARD + a_bytes, d_size: int = GUARD + d_bytes) -> int:
