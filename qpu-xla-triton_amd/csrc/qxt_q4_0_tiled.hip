@@ -300,7 +300,17 @@ __device__ __forceinline__ void stage_pair(int q, int &row, int &jb) {
 }
 
 // Rows past M, columns past N and blocks past K load zeros (out-of-range
-// offsets), so their values and scales stage as zeros.
+// offsets), so their values and scales stage as zeros.  SELECT computes every
+// lane's offset and then selects it (no control flow in the loop); otherwise
+// the offset is computed only under the condition, which the compiler turns
+// into a branch around the weight offset.  The branch splits the loop body:
+// the group's four MFMAs are then issued before any of its scaling, and all
+// four blocks' dots and scales stay live (178 VGPRs: two workgroups per CU).
+// The select form keeps the dots of one block ahead (155 VGPRs: three
+// workgroups per CU).  Measured on MI355X at M = 512: K=2048 N=5632 (704
+// workgroups) 43.0 -> 38.5 us with SELECT; K=5632 N=2048 (256 workgroups, one
+// wave per SIMD) 48.7 us without, 56 us with.
+template <bool SELECT>
 __device__ __forceinline__ void stage_load(const TiledArgs &t, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rw,
                                            int m0, int n0, int g0, StageRegs &r) {
 #pragma unroll
@@ -308,9 +318,14 @@ __device__ __forceinline__ void stage_load(const TiledArgs &t, __amdgpu_buffer_r
         int row, jb;
         stage_pair(q, row, jb);
         const int b = g0 + jb, m = m0 + row;
-        const uint32_t o = b < t.blocks && m < t.m
-                               ? static_cast<uint32_t>(m) * t.act_stride + static_cast<uint32_t>(b) * 34u
-                               : kOutOfRange;
+        uint32_t o;
+        if constexpr (SELECT) {
+            const uint32_t raw = static_cast<uint32_t>(m) * t.act_stride + static_cast<uint32_t>(b) * 34u;
+            o = ((b < t.blocks) & (m < t.m)) ? raw : kOutOfRange;
+        } else {
+            o = b < t.blocks && m < t.m ? static_cast<uint32_t>(m) * t.act_stride + static_cast<uint32_t>(b) * 34u
+                                        : kOutOfRange;
+        }
         const uint32_t v = (o + 2) & ~3u;  // the 32 values start 2 bytes in
         const v4u x0 = __builtin_amdgcn_raw_buffer_load_b128(ra, v, 0, 0);
         const v4u x1 = __builtin_amdgcn_raw_buffer_load_b128(ra, v + 16, 0, 0);
@@ -331,9 +346,15 @@ __device__ __forceinline__ void stage_load(const TiledArgs &t, __amdgpu_buffer_r
         int col, jb;
         stage_pair(q, col, jb);
         const int b = g0 + jb, n = n0 + col;
-        const uint32_t o = b < t.blocks && n < t.n
-                               ? static_cast<uint32_t>(t.wcol0 + n) * t.w_stride + static_cast<uint32_t>(b) * 18u
-                               : kOutOfRange;
+        uint32_t o;
+        if constexpr (SELECT) {
+            const uint32_t raw = static_cast<uint32_t>(t.wcol0 + n) * t.w_stride + static_cast<uint32_t>(b) * 18u;
+            o = ((b < t.blocks) & (n < t.n)) ? raw : kOutOfRange;
+        } else {
+            o = b < t.blocks && n < t.n
+                    ? static_cast<uint32_t>(t.wcol0 + n) * t.w_stride + static_cast<uint32_t>(b) * 18u
+                    : kOutOfRange;
+        }
         const uint32_t v = (o + 2) & ~3u;  // the 16 nibble bytes start 2 bytes in
         const v4u x0 = __builtin_amdgcn_raw_buffer_load_b128(rw, v, 0, 0);
 #pragma unroll
@@ -376,6 +397,7 @@ __device__ __forceinline__ void stage_store(const StageRegs &r, StageBuf &s) {
     }
 }
 
+template <bool SELECT>
 __global__ __launch_bounds__(kThreads) void q4_0_staged_kernel(TiledArgs t) {
     __shared__ __attribute__((aligned(16))) StageBuf stage[2];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -395,9 +417,9 @@ __global__ __launch_bounds__(kThreads) void q4_0_staged_kernel(TiledArgs t) {
     const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
     StageRegs regs;
-    stage_load(t, ra, rw, m0, n0, 0, regs);
+    stage_load<SELECT>(t, ra, rw, m0, n0, 0, regs);
     stage_store(regs, stage[0]);
-    stage_load(t, ra, rw, m0, n0, kGroup, regs);
+    stage_load<SELECT>(t, ra, rw, m0, n0, kGroup, regs);
     __syncthreads();
 
     auto frag = [&](const StageBuf &s, int j, v4i &a, v4i &w) {
@@ -452,7 +474,7 @@ __global__ __launch_bounds__(kThreads) void q4_0_staged_kernel(TiledArgs t) {
         // The other buffer was last read a group ago (before the previous
         // barrier): fill it with the next group and load the one after.
         stage_store(regs, stage[buf ^ 1]);
-        stage_load(t, ra, rw, m0, n0, g0 + 2 * kGroup, regs);
+        stage_load<SELECT>(t, ra, rw, m0, n0, g0 + 2 * kGroup, regs);
         __syncthreads();
     }
     if (bn >= t.n) return;
@@ -474,7 +496,12 @@ int launch_tiled(const TiledArgs &t, bool native, hipStream_t stream) {
     // fragments sit at 2-byte offsets, one scattered row per lane); the split
     // planes are read as fragments directly (measured on MI355X at M = 512:
     // native gate_up 103 -> 42 us staged; split 44 us direct, 64 us staged).
-    if (native) return launch("q4_0_tiled_kernel", q4_0_staged_kernel, grid, dim3(kThreads), 0, stream, t);
+    if (native) {
+        const long workgroups = static_cast<long>(grid.x) * grid.y;
+        if (workgroups >= 2L * compute_units())
+            return launch("q4_0_tiled_kernel", q4_0_staged_kernel<true>, grid, dim3(kThreads), 0, stream, t);
+        return launch("q4_0_tiled_kernel", q4_0_staged_kernel<false>, grid, dim3(kThreads), 0, stream, t);
+    }
     if (t.cs != nullptr) return launch("q4_0_tiled_kernel", q4_0_tiled_kernel<true>, grid, dim3(kThreads), 0, stream, t);
     return launch("q4_0_tiled_kernel", q4_0_tiled_kernel<false>, grid, dim3(kThreads), 0, stream, t);
 }
