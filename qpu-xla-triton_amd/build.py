@@ -42,11 +42,13 @@ HIPCC_FLAGS = [
 ]
 
 
-# Per-source additions.  The prefill kernel converts every matrix-core result
-# with VALU instructions, so its MFMAs write VGPRs directly (no accumulator-
-# register copies); the W8A8 GEMM keeps its 256 accumulators in AGPRs.
+# Per-source additions.  The prefill kernel and the four-row decode tiles
+# convert every matrix-core result with VALU instructions, so their MFMAs
+# write VGPRs directly (no accumulator-register copies); the W8A8 GEMM keeps
+# its 256 accumulators in AGPRs.
 SOURCE_FLAGS = {
     "qxt_q4_0_tiled.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "qxt_q4_0.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

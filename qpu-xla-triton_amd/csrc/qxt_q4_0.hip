@@ -48,6 +48,7 @@
 #include <algorithm>
 #include <new>
 #include <type_traits>
+#include <utility>
 #include <vector>
 
 #include "qxt_common.h"
@@ -161,10 +162,28 @@ __device__ __forceinline__ int block_dot(const uint32_t (&qs)[4], const int *aq,
     return block_dot(qs, *reinterpret_cast<const int4 *>(aq), *reinterpret_cast<const int4 *>(aq + 4), asum);
 }
 
+// The (scale, sum) record of block b of LDS row r.  Row-major by default:
+// the pair (d, sum(a)) at ad[r * ad_row + ad_index(b)].  SCALES4 (the
+// four-row matrix-core tiles) keeps the four rows of a block together
+// instead: -8 * sum(a) of rows 0..3 at ad[aq_index(b, 0 .. 3)], d of rows
+// 0..3 at ad[aq_index(b, 4 .. 7)], so one lane reads a block's records for
+// all four rows with two 16-byte loads.
+template <bool SCALES4>
+__device__ __forceinline__ void store_scale_sum(int *ad, const Q4Lds &geo, int r, int b, float d, int sum) {
+    if constexpr (SCALES4) {
+        ad[aq_index(b, r)] = -8 * sum;
+        ad[aq_index(b, 4 + r)] = __float_as_int(d);
+    } else {
+        ad[r * geo.ad_row + ad_index(b)] = __float_as_int(d);
+        ad[r * geo.ad_row + ad_index(b) + 1] = sum;
+    }
+}
+
 // Quantise element chunk e (float4 v: elements 4 (e % 8) .. of block e / 8 of
 // row r) by the rule of q8_0_prepass_kernel -- 8 lanes per block, the dots use
 // the fp16-rounded d -- into the LDS activation of row r; nothing is stored
 // when `store` is false.  The 8 lanes of a block must be active together.
+template <bool SCALES4 = false>
 __device__ __forceinline__ void quantise_chunk(const float4 &v, int r, int rem, int *aq, int *ad, const Q4Lds &geo,
                                                bool store = true) {
     const int b = rem >> 3, l8 = rem & 7;
@@ -182,10 +201,7 @@ __device__ __forceinline__ void quantise_chunk(const float4 &v, int r, int rem, 
     sum += __shfl_xor(sum, 4, 8);
     if (!store) return;
     aq[r * geo.aq_row + aq_index(b, l8)] = static_cast<int>(pack_bytes(q0, q1, q2, q3));
-    if (l8 == 0) {
-        ad[r * geo.ad_row + ad_index(b)] = __float_as_int(half_bits_to_float(float_to_half_bits(d)));
-        ad[r * geo.ad_row + ad_index(b) + 1] = sum;
-    }
+    if (l8 == 0) store_scale_sum<SCALES4>(ad, geo, r, b, half_bits_to_float(float_to_half_bits(d)), sum);
 }
 
 // A one-row fp32 activation of K <= kMaxPrefetchChunks * 4 * kThreads
@@ -227,8 +243,9 @@ __device__ __forceinline__ void quantise_row(const Q4Task &t, const float4 (&xv)
     }
 }
 
-// Stage the activation rows r0 .. r0+MR-1 of `t` into LDS (rows >= t.rows become zeros).
-template <int MR>
+// Stage the activation rows r0 .. r0+MR-1 of `t` into LDS (rows >= t.rows
+// become zeros), the (scale, sum) records in the layout of store_scale_sum.
+template <int MR, bool SCALES4 = false>
 __device__ __forceinline__ void stage_activation(const Q4Task &t, int r0, int *aq, int *ad, const Q4Lds &geo) {
     const int B = t.blocks;
     if (t.x != nullptr) {
@@ -254,7 +271,7 @@ __device__ __forceinline__ void stage_activation(const Q4Task &t, int r0, int *a
                 const int e = base + u * kThreads + threadIdx.x;
                 if (e >= total) break;
                 const int r = e / (B * 8);
-                quantise_chunk(v[u], r, e - r * B * 8, aq, ad, geo);
+                quantise_chunk<SCALES4>(v[u], r, e - r * B * 8, aq, ad, geo);
             }
         }
         return;
@@ -279,8 +296,58 @@ __device__ __forceinline__ void stage_activation(const Q4Task &t, int r0, int *a
         int *dstq = aq + r * geo.aq_row + aq_index(b, 0);
 #pragma unroll
         for (int j = 0; j < 8; ++j) dstq[j] = words[j];
-        ad[r * geo.ad_row + ad_index(b)] = __float_as_int(d);
-        ad[r * geo.ad_row + ad_index(b) + 1] = sum;
+        store_scale_sum<SCALES4>(ad, geo, r, b, d, sum);
+    }
+}
+
+// Native Q8_0 activation rows of a four-row group for the matrix-core
+// tiles, requested into registers before any weight load: two (row, block)
+// items per thread (4 * blocks <= 512), 17 half-words each.  The loads are
+// unconditional (indexes clamped into the activation), so the compiler
+// counts the weight loads issued after them exactly and the staging waits
+// only for these.
+struct Q8RowRegs {
+    uint32_t h[2][17];
+};
+
+__device__ __forceinline__ void fetch_q8_rows(const Q4Task &t, int r0, Q8RowRegs &a) {
+    const int B = t.blocks;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int idx = min(static_cast<int>(threadIdx.x) + i * kThreads, 4 * B - 1);
+        const int r = idx / B;
+        const int b = idx - r * B;
+        const int row = min(r0 + r, t.rows - 1);
+        const QXT_GLOBAL uint16_t *p =
+            global_in<uint16_t>(t.act + row * t.act_stride + static_cast<size_t>(b) * Q8_0_BYTES);
+#pragma unroll
+        for (int k = 0; k < 17; ++k) a.h[i][k] = p[k];
+    }
+}
+
+// The LDS image of fetch_q8_rows' items, the records in the SCALES4 layout.
+// A row past t.rows holds a copy of the last row: a matrix-core output row
+// depends on its own activation row only, and those rows are never stored.
+__device__ __forceinline__ void stage_q8_rows(const Q4Task &t, const Q8RowRegs &a, int *aq, int *ad,
+                                              const Q4Lds &geo) {
+    const int B = t.blocks;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int idx = static_cast<int>(threadIdx.x) + i * kThreads;
+        if (idx >= 4 * B) break;
+        const int r = idx / B;
+        const int b = idx - r * B;
+        int words[8];
+        int sum = 0;
+#pragma unroll
+        for (int h = 0; h < 8; ++h) {
+            words[h] = static_cast<int>(a.h[i][1 + 2 * h] | (a.h[i][2 + 2 * h] << 16));
+            sum = dot4(words[h], 0x01010101, sum);  // sum of the four signed bytes
+        }
+        int *dstq = aq + r * geo.aq_row + aq_index(b, 0);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dstq[j] = words[j];
+        store_scale_sum<true>(ad, geo, r, b, half_bits_to_float(a.h[i][0]), sum);
     }
 }
 
@@ -296,6 +363,38 @@ enum WeightLayout { kNativeRows = 0, kLaneLayout = 1, kEitherLayout = 2 };
 // for an earlier load (a prefetched activation) does not wait for these.
 // Without CLAMP, lanes past the tile skip their loads (cheaper for small
 // tiles when nothing loaded earlier is waited for).
+// Units of the four-row matrix-core path: in a wave of 64 consecutive units
+// starting at a column boundary, lane 4 b + p takes column 4 (b / G) + p,
+// block range b % G (G divides 16), so that every
+// 4-lane block of v_mfma_i32_4x4x4_16b_i8 holds four columns of one block
+// range.  The 64 units of a wave are the same, only permuted across lanes:
+// each load instruction still reads one contiguous kilobyte of the lane
+// layout.
+// load_units of the matrix-core tiles: lane layout, units in mfma4_unit
+// order, every lane loading (CLAMP), G = 1 << lg.
+template <int U>
+__device__ __forceinline__ void load_units_m4(const Q4Task &t, int col_base, int lg, int units, int first,
+                                              uint32_t (&d)[U][36]) {
+    const int lane = threadIdx.x & 63;
+    const int b = lane >> 2, p = lane & 3;
+    const int perm = ((((b >> lg) << 2) + p) << lg) + (b & ((1 << lg) - 1));
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+        const int u = min(first + j * kThreads + (static_cast<int>(threadIdx.x) & ~63) + perm, units - 1);
+        const size_t unit = (static_cast<size_t>(t.wcol0 + col_base + (u >> lg)) << lg) + (u & ((1 << lg) - 1));
+        const QXT_GLOBAL v4u *src =
+            global_in<v4u>(t.w + (unit / kLaneGroup) * kGroupBytes + (unit % kLaneGroup) * 16);
+#pragma unroll
+        for (int v = 0; v < 9; ++v) {
+            const v4u x = __builtin_nontemporal_load(src + v * kLaneGroup);
+            d[j][4 * v + 0] = x[0];
+            d[j][4 * v + 1] = x[1];
+            d[j][4 * v + 2] = x[2];
+            d[j][4 * v + 3] = x[3];
+        }
+    }
+}
+
 template <int U, int LAYOUT = kEitherLayout, bool CLAMP = false>
 __device__ __forceinline__ void load_units(const Q4Task &t, int col_base, int G, int units, int first,
                                            uint32_t (&d)[U][36]) {
@@ -490,6 +589,74 @@ __device__ __forceinline__ void compute_fast(const Q4Task &t, int col_base, int 
     }
 }
 
+// Phase 2 of the four-row lane-layout path on the matrix cores: the units of
+// one round in mfma4_unit order.  Per Q4_0 block, eight
+// v_mfma_i32_4x4x4_16b_i8 (K = 4 each) give every lane the exact dots of its
+// column with the four activation rows: operand A is activation row p of the
+// lane's block range (lane 4 b + p), operand B the lane's own nibbles as
+// unsigned codes, the accumulator starting from -8 * sum(a) of each row (the
+// SCALES4 records), so every lane ends with the same exact signed dots as the
+// v_dot4 path and the block terms are the same bits.
+template <int U>
+__device__ __forceinline__ void compute_mfma4(const Q4Task &t, int lg, int units, int first,
+                                              const uint32_t (&wr)[U][36], const int *aq, const int *ad, float *cb,
+                                              const Q4Lds &geo) {
+    typedef int v4i_t __attribute__((ext_vector_type(4)));
+    const int lane = threadIdx.x & 63;
+    const int b = lane >> 2, p = lane & 3;
+    const int g = b & ((1 << lg) - 1);
+    const int *arow = aq + p * geo.aq_row;
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+        const int u = first + j * kThreads + (static_cast<int>(threadIdx.x) & ~63) + ((((b >> lg) << 2) + p) << lg) + g;
+        const int col = u >> lg;
+        float terms[4][8];
+        auto do_block = [&](auto ic) {
+            constexpr int I = decltype(ic)::value;
+            uint32_t sbits, qs[4];
+            unit_block<I>(wr[j], sbits, qs);
+            const int bg = g * 8 + I;
+            const int4 lo = *reinterpret_cast<const int4 *>(arow + aq_index(bg, 0));
+            const int4 hi = *reinterpret_cast<const int4 *>(arow + aq_index(bg, 4));
+            const int4 s8 = *reinterpret_cast<const int4 *>(ad + aq_index(bg, 0));
+            const float4 da = *reinterpret_cast<const float4 *>(ad + aq_index(bg, 4));
+            v4i_t acc = {s8.x, s8.y, s8.z, s8.w};
+            acc = __builtin_amdgcn_mfma_i32_4x4x4i8(lo.x, static_cast<int>(qs[0] & 0x0F0F0F0Fu), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_i32_4x4x4i8(lo.y, static_cast<int>(qs[1] & 0x0F0F0F0Fu), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_i32_4x4x4i8(lo.z, static_cast<int>(qs[2] & 0x0F0F0F0Fu), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_i32_4x4x4i8(lo.w, static_cast<int>(qs[3] & 0x0F0F0F0Fu), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_i32_4x4x4i8(hi.x, static_cast<int>((qs[0] >> 4) & 0x0F0F0F0Fu), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_i32_4x4x4i8(hi.y, static_cast<int>((qs[1] >> 4) & 0x0F0F0F0Fu), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_i32_4x4x4i8(hi.z, static_cast<int>((qs[2] >> 4) & 0x0F0F0F0Fu), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_i32_4x4x4i8(hi.w, static_cast<int>((qs[3] >> 4) & 0x0F0F0F0Fu), acc, 0, 0, 0);
+            const float dw = half_bits_to_float(sbits);
+            const float das[4] = {da.x, da.y, da.z, da.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v = static_cast<float>(acc[r]) * dw;
+                v = v * das[r];
+                terms[r][I] = v;
+            }
+        };
+        do_block(std::integral_constant<int, 0>{});
+        do_block(std::integral_constant<int, 1>{});
+        do_block(std::integral_constant<int, 2>{});
+        do_block(std::integral_constant<int, 3>{});
+        do_block(std::integral_constant<int, 4>{});
+        do_block(std::integral_constant<int, 5>{});
+        do_block(std::integral_constant<int, 6>{});
+        do_block(std::integral_constant<int, 7>{});
+        if (u < units) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float4 *c4 = reinterpret_cast<float4 *>(cb + (r * t.cpw + col) * geo.cbs + g * 8);
+                c4[0] = make_float4(terms[r][0], terms[r][1], terms[r][2], terms[r][3]);
+                c4[1] = make_float4(terms[r][4], terms[r][5], terms[r][6], terms[r][7]);
+            }
+        }
+    }
+}
+
 // Phase 3: one thread per (row, column) adds the column's block terms in
 // block order and stores the fp32 result.
 template <int MR, bool FAST>
@@ -519,8 +686,10 @@ __device__ __forceinline__ void sum_store(const Q4Task &t, int col_base, int r0,
 }
 
 // One linear: workgroup (x, y) owns columns [x * cpw, +cpw) and rows [y * MR, +MR).
-template <int MR, int U, bool FAST, bool DOTS, int LAYOUT = kNativeRows>
+// MFMA4: four-row lane-layout tiles on the matrix cores (compute_mfma4).
+template <int MR, int U, bool FAST, bool DOTS, int LAYOUT = kNativeRows, bool MFMA4 = false>
 __global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Task t) {
+    static_assert(!MFMA4 || (MR == 4 && FAST && !DOTS && LAYOUT == kLaneLayout), "matrix-core tiles: four rows, lanes");
     extern __shared__ int lds[];
     const int col_base = blockIdx.x * t.cpw;
     const int r0 = blockIdx.y * MR;
@@ -534,6 +703,39 @@ __global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Task t) {
     const int G = FAST ? (B >> 3) : B;
     const int units = tile_cols * G;
     uint32_t wr[FAST ? U : 1][36];
+
+    if constexpr (MFMA4) {
+        // The activation first, then two rounds of weights, so that the
+        // staging waits only for the activation and the weight stream runs
+        // through it.  The loads of every round are unconditional (lanes
+        // past the tile re-read its last unit), so the compiler counts them
+        // exactly in every wait.
+        Q8RowRegs a;
+        fetch_q8_rows(t, r0, a);
+        __builtin_amdgcn_sched_barrier(0);  // keep the activation loads first
+        uint32_t wn[U][36];
+        const int lg = __builtin_ctz(G);
+        load_units_m4<U>(t, col_base, lg, units, 0, wr);
+        load_units_m4<U>(t, col_base, lg, units, U * kThreads, wn);
+        __builtin_amdgcn_sched_barrier(0);
+        stage_q8_rows(t, a, aq, ad, geo);
+        __syncthreads();
+        // Two register sets in turn (no copies between them): each is
+        // refilled with the round after next as soon as it is computed.
+        constexpr int R = U * kThreads;
+        for (int first = 0;;) {
+            compute_mfma4<U>(t, lg, units, first, wr, aq, ad, cb, geo);
+            load_units_m4<U>(t, col_base, lg, units, first + 2 * R, wr);
+            if ((first += R) >= units) break;
+            compute_mfma4<U>(t, lg, units, first, wn, aq, ad, cb, geo);
+            load_units_m4<U>(t, col_base, lg, units, first + 2 * R, wn);
+            if ((first += R) >= units) break;
+        }
+        __syncthreads();
+        sum_store<MR, FAST>(t, col_base, r0, tile_cols, cb, geo);
+        return;
+    }
+
     if constexpr (FAST) load_units<U, LAYOUT>(t, col_base, G, units, 0, wr);
 
     stage_activation<MR>(t, r0, aq, ad, geo);
@@ -646,6 +848,7 @@ constexpr int kPrefetchUnits = QXT_PREFETCH_UNITS;
 #define QXT_PREFETCH_LARGE 0
 #endif
 constexpr bool kPrefetchLargeBatches = QXT_PREFETCH_LARGE != 0;
+
 static_assert(kPrefetchUnits >= 1 && kPrefetchUnits <= units_per_thread(1),
               "a prefetch plan must fit the one-row batch kernel it falls back to");
 
@@ -706,6 +909,15 @@ int launch_single(Q4Task t, hipStream_t stream) {
     constexpr int U = units_per_thread(MR);
     const char *name = DOTS ? "q4_0_block_dots_kernel" : "q4_0_linear_kernel";
     if constexpr (!DOTS) {
+        // Four rows over the lane layout with a block range per unit that
+        // divides 16 (K <= 4096): the matrix-core tiles (measured on MI355X,
+        // cfg2 back to back: 12.9 -> 9.6 us at N = 11008 and 7.4 -> 5.5 us
+        // at N = 4096 against the v_dot4 wide tiles).
+        const int G = t.blocks / 8;
+        if constexpr (MR == 4)
+            if (fast && t.lanes && t.x == nullptr && G <= 16 && 16 % G == 0)
+                return launch(name, q4_0_linear_kernel<MR, U, true, false, kLaneLayout, true>, grid, dim3(kThreads),
+                              lds, stream, t);
         if (fast && t.lanes)
             return launch(name, q4_0_linear_kernel<MR, U, true, false, kLaneLayout>, grid, dim3(kThreads), lds, stream,
                           t);

@@ -362,6 +362,11 @@ def test_lane_pack_kernel_matches_the_layout_definition(n: int, blocks: int) -> 
     (17, 512, 64, 0, 64),       # rows beyond one MFMA-free row group
     (4, 14336, 1024, 0, 1024),  # K = 14336 at four rows: one-column tiles above 64 KB of LDS
     (8, 14336, 512, 16, 496),   # two row groups at K = 14336
+    # four-row matrix-core tiles at every block range per unit that divides 16
+    (4, 256, 37, 5, 31),        # one block range per unit, ragged
+    (6, 512, 130, 2, 128),      # two, a partial second row group
+    (5, 1024, 200, 3, 190),     # four, one row in the second row group
+    (4, 2048, 300, 0, 300),     # eight
 ])
 def test_lane_linear_bit_exact_against_oracle(rows: int, k: int, n: int, wcol0: int, ncols: int) -> None:
     rng = np.random.default_rng(5000 + rows + n)
