@@ -202,7 +202,9 @@ int qxt_q4_0_pack_lanes(const void *weight, size_t weight_row_stride, void *pack
 
 /* qxt_ggml_q4_0_q8_0_linear over a lane-layout weight of `weight_columns`
  * columns (weight_column_start + column_count <= weight_columns); same
- * result bit for bit.  Any row count runs on v_dot4. */
+ * result bit for bit.  Four or more rows with blocks / 8 dividing 16 (K <= 4096)
+ * run on v_mfma_i32_4x4x4_16b_i8 (four rows x four columns per 4-lane block);
+ * other shapes on v_dot4. */
 int qxt_ggml_q4_0_q8_0_linear_lanes(const void *activation, size_t activation_row_stride,
                                     const void *packed_weight, uint32_t weight_columns,
                                     float *destination, size_t destination_row_stride,
