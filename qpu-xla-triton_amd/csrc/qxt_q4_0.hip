@@ -370,9 +370,10 @@ enum WeightLayout { kNativeRows = 0, kLaneLayout = 1, kEitherLayout = 2 };
 // range.  The 64 units of a wave are the same, only permuted across lanes:
 // each load instruction still reads one contiguous kilobyte of the lane
 // layout.
-// load_units of the matrix-core tiles: lane layout, units in mfma4_unit
-// order, every lane loading (CLAMP), G = 1 << lg.
-template <int U>
+// load_units of the matrix-core tiles: units in mfma4_unit order, every
+// lane loading (CLAMP), G = 1 << lg.  Lane layout: one contiguous kilobyte
+// per wave instruction, non-temporal; native rows: each lane's 144 bytes.
+template <int U, int LAYOUT>
 __device__ __forceinline__ void load_units_m4(const Q4Task &t, int col_base, int lg, int units, int first,
                                               uint32_t (&d)[U][36]) {
     const int lane = threadIdx.x & 63;
@@ -381,16 +382,30 @@ __device__ __forceinline__ void load_units_m4(const Q4Task &t, int col_base, int
 #pragma unroll
     for (int j = 0; j < U; ++j) {
         const int u = min(first + j * kThreads + (static_cast<int>(threadIdx.x) & ~63) + perm, units - 1);
-        const size_t unit = (static_cast<size_t>(t.wcol0 + col_base + (u >> lg)) << lg) + (u & ((1 << lg) - 1));
-        const QXT_GLOBAL v4u *src =
-            global_in<v4u>(t.w + (unit / kLaneGroup) * kGroupBytes + (unit % kLaneGroup) * 16);
+        const int col = u >> lg, g = u & ((1 << lg) - 1);
+        if constexpr (LAYOUT == kLaneLayout) {
+            const size_t unit = (static_cast<size_t>(t.wcol0 + col_base + col) << lg) + g;
+            const QXT_GLOBAL v4u *src =
+                global_in<v4u>(t.w + (unit / kLaneGroup) * kGroupBytes + (unit % kLaneGroup) * 16);
 #pragma unroll
-        for (int v = 0; v < 9; ++v) {
-            const v4u x = __builtin_nontemporal_load(src + v * kLaneGroup);
-            d[j][4 * v + 0] = x[0];
-            d[j][4 * v + 1] = x[1];
-            d[j][4 * v + 2] = x[2];
-            d[j][4 * v + 3] = x[3];
+            for (int v = 0; v < 9; ++v) {
+                const v4u x = __builtin_nontemporal_load(src + v * kLaneGroup);
+                d[j][4 * v + 0] = x[0];
+                d[j][4 * v + 1] = x[1];
+                d[j][4 * v + 2] = x[2];
+                d[j][4 * v + 3] = x[3];
+            }
+        } else {
+            const QXT_GLOBAL v4u *src = global_in<v4u>(
+                t.w + static_cast<size_t>(t.wcol0 + col_base + col) * t.w_stride + static_cast<size_t>(g) * 144);
+#pragma unroll
+            for (int v = 0; v < 9; ++v) {
+                const v4u x = src[v];
+                d[j][4 * v + 0] = x[0];
+                d[j][4 * v + 1] = x[1];
+                d[j][4 * v + 2] = x[2];
+                d[j][4 * v + 3] = x[3];
+            }
         }
     }
 }
@@ -689,7 +704,7 @@ __device__ __forceinline__ void sum_store(const Q4Task &t, int col_base, int r0,
 // MFMA4: four-row lane-layout tiles on the matrix cores (compute_mfma4).
 template <int MR, int U, bool FAST, bool DOTS, int LAYOUT = kNativeRows, bool MFMA4 = false>
 __global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Task t) {
-    static_assert(!MFMA4 || (MR == 4 && FAST && !DOTS && LAYOUT == kLaneLayout), "matrix-core tiles: four rows, lanes");
+    static_assert(!MFMA4 || (MR == 4 && FAST && !DOTS && LAYOUT != kEitherLayout), "matrix-core tiles: four rows");
     extern __shared__ int lds[];
     const int col_base = blockIdx.x * t.cpw;
     const int r0 = blockIdx.y * MR;
@@ -715,8 +730,8 @@ __global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Task t) {
         __builtin_amdgcn_sched_barrier(0);  // keep the activation loads first
         uint32_t wn[U][36];
         const int lg = __builtin_ctz(G);
-        load_units_m4<U>(t, col_base, lg, units, 0, wr);
-        load_units_m4<U>(t, col_base, lg, units, U * kThreads, wn);
+        load_units_m4<U, LAYOUT>(t, col_base, lg, units, 0, wr);
+        load_units_m4<U, LAYOUT>(t, col_base, lg, units, U * kThreads, wn);
         __builtin_amdgcn_sched_barrier(0);
         stage_q8_rows(t, a, aq, ad, geo);
         __syncthreads();
@@ -725,10 +740,10 @@ __global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Task t) {
         constexpr int R = U * kThreads;
         for (int first = 0;;) {
             compute_mfma4<U>(t, lg, units, first, wr, aq, ad, cb, geo);
-            load_units_m4<U>(t, col_base, lg, units, first + 2 * R, wr);
+            load_units_m4<U, LAYOUT>(t, col_base, lg, units, first + 2 * R, wr);
             if ((first += R) >= units) break;
             compute_mfma4<U>(t, lg, units, first, wn, aq, ad, cb, geo);
-            load_units_m4<U>(t, col_base, lg, units, first + 2 * R, wn);
+            load_units_m4<U, LAYOUT>(t, col_base, lg, units, first + 2 * R, wn);
             if ((first += R) >= units) break;
         }
         __syncthreads();
@@ -909,15 +924,17 @@ int launch_single(Q4Task t, hipStream_t stream) {
     constexpr int U = units_per_thread(MR);
     const char *name = DOTS ? "q4_0_block_dots_kernel" : "q4_0_linear_kernel";
     if constexpr (!DOTS) {
-        // Four rows over the lane layout with a block range per unit that
-        // divides 16 (K <= 4096): the matrix-core tiles (measured on MI355X,
-        // cfg2 back to back: 12.9 -> 9.6 us at N = 11008 and 7.4 -> 5.5 us
+        // Four rows with a block range per unit that divides 16 (K <= 4096):
+        // the matrix-core tiles (measured on MI355X, cfg2 over lane-layout
+        // weights back to back: 12.9 -> 9.6 us at N = 11008 and 7.4 -> 5.5 us
         // at N = 4096 against the v_dot4 wide tiles).
         const int G = t.blocks / 8;
         if constexpr (MR == 4)
-            if (fast && t.lanes && t.x == nullptr && G <= 16 && 16 % G == 0)
-                return launch(name, q4_0_linear_kernel<MR, U, true, false, kLaneLayout, true>, grid, dim3(kThreads),
-                              lds, stream, t);
+            if (fast && t.x == nullptr && G <= 16 && 16 % G == 0)
+                return t.lanes ? launch(name, q4_0_linear_kernel<MR, U, true, false, kLaneLayout, true>, grid,
+                                        dim3(kThreads), lds, stream, t)
+                               : launch(name, q4_0_linear_kernel<MR, U, true, false, kNativeRows, true>, grid,
+                                        dim3(kThreads), lds, stream, t);
         if (fast && t.lanes)
             return launch(name, q4_0_linear_kernel<MR, U, true, false, kLaneLayout>, grid, dim3(kThreads), lds, stream,
                           t);

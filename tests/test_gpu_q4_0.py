@@ -73,6 +73,8 @@ def test_reference_seed_fixture_bit_exact_and_block_dots() -> None:
         (1, 1024, 16),   # K=32768: 128 units per column, two columns per workgroup
         (4, 128, 11000),  # four rows, wide tiles: 43 columns per workgroup in three rounds, ragged last tile
         (8, 128, 4100),   # two row groups of wide tiles, three rounds per workgroup
+        (6, 16, 130),     # four-row matrix-core tiles over native rows, two block ranges per unit
+        (4, 32, 77),      # four block ranges per unit
     ],
 )
 def test_random_shapes_bit_exact(rows: int, blocks: int, outputs: int) -> None:
