@@ -126,6 +126,21 @@ __device__ __forceinline__ int quant_div(float v, float s) {
     return s > 0.0f ? clamp127(rintf(v / s)) : 0;
 }
 
+// quant_div for a whole row from its scale's reciprocal r = fl(1 / s) (IEEE
+// division, once per row): q0 = fl(v r) is within an ulp of v / s, the
+// residual fma(-q0, s, v) is exact, and fma(residual, r, q0) is the IEEE
+// quotient fl(v / s) (Markstein's theorem: a correctly rounded reciprocal and
+// one fused correction step give the correctly rounded quotient when nothing
+// underflows).  kRecipScaleMin keeps every nonzero residual that can move a
+// quotient of magnitude >= 1/4 in the normal range (smaller quotients round
+// to 0 either way); below it, and for s = 0, use quant_div.
+constexpr float kRecipScaleMin = 0x1p-70f;
+__device__ __forceinline__ int quant_recip(float v, float s, float r) {
+    const float q0 = v * r;
+    const float e = fmaf(-q0, s, v);
+    return clamp127(rintf(fmaf(e, r, q0)));
+}
+
 __device__ __forceinline__ uint32_t pack_bytes(int q0, int q1, int q2, int q3) {
     return (static_cast<uint32_t>(q0) & 0xFFu) | ((static_cast<uint32_t>(q1) & 0xFFu) << 8) |
            ((static_cast<uint32_t>(q2) & 0xFFu) << 16) | ((static_cast<uint32_t>(q3) & 0xFFu) << 24);

@@ -290,12 +290,17 @@ __global__ __launch_bounds__(kThreads) void rows_int8_kernel(const float *__rest
         }
     }
     const float s = row_scale(block_max(amax, scratch), floor);
+    // Every row scale of the 1/127 floor takes the reciprocal form (measured
+    // on MI355X at 4096 rows: K = 14336 50.8 -> 47.0 us, K = 4096 15.6 ->
+    // 14.4 us against a division per element).
+    const bool recip = s >= kRecipScaleMin;
+    const float r = recip ? 1.0f / s : 0.0f;
+    auto quant = [&](float x) { return recip ? quant_recip(x, s, r) : quant_div(x, s); };
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const uint32_t c = threadIdx.x + i * kThreads;
         if (c < chunks) {
-            const uint32_t word = pack_bytes(quant_div(v[i].x, s), quant_div(v[i].y, s), quant_div(v[i].z, s),
-                                             quant_div(v[i].w, s));
+            const uint32_t word = pack_bytes(quant(v[i].x), quant(v[i].y), quant(v[i].z), quant(v[i].w));
             if constexpr (VEC) {
                 *reinterpret_cast<uint32_t *>(dst + 4 * c) = word;
             } else {

@@ -68,6 +68,50 @@ def test_rows_int8_outlier_channels_like_cfg4() -> None:
     np.testing.assert_array_equal(s.cpu().numpy(), sr)
 
 
+def _near_half_integer_rows(rng, scales: np.ndarray, cols: int) -> np.ndarray:
+    """Rows whose scale is fl32(fl32(127 t) / 127) for each target t, filled with
+    fl32((k + 1/2) s) moved by -3..3 ulps: quotients at and beside rounding ties."""
+    rows = len(scales)
+    x = np.empty((rows, cols), np.float32)
+    for i, t in enumerate(scales.astype(np.float32)):
+        amax = np.float32(np.float32(127.0) * t)
+        s = np.float32(amax / np.float32(127.0))
+        k = rng.integers(-127, 127, cols - 1)
+        v = ((k.astype(np.float64) + 0.5) * np.float64(s)).astype(np.float32)
+        steps = rng.integers(-3, 4, cols - 1)
+        v = np.nextafter(v, np.where(steps > 0, np.inf, -np.inf).astype(np.float32))
+        for _ in range(2):
+            more = np.abs(steps) > 1
+            v[more] = np.nextafter(v[more], np.where(steps[more] > 0, np.inf, -np.inf).astype(np.float32))
+            steps = np.where(more, steps - np.sign(steps), steps)
+        v[steps == 0] = ((k[steps == 0].astype(np.float64) + 0.5) * np.float64(s)).astype(np.float32)
+        x[i, 0] = amax
+        x[i, 1:] = np.clip(v, -amax, amax)
+    return x
+
+
+def test_rows_int8_quotients_at_rounding_ties_bit_exact() -> None:
+    # The quantiser divides by the row scale through its reciprocal with one
+    # fused correction step; every quotient must still round as IEEE x / s.
+    rng = np.random.default_rng(77)
+    sig = rng.integers(1 << 23, 1 << 24, 64)
+    sig[:8] = (1 << 24) - 1  # all-ones significands
+    sig[8:12] = 1 << 23
+    scales = (sig.astype(np.float64) * np.exp2(rng.integers(-6, 10, 64) - 23)).astype(np.float32)
+    x = _near_half_integer_rows(rng, scales, 4096)
+    q, s = quantize_rows_int8(dev(x))
+    qr, sr = oracle.quantize_rows_int8(x)
+    np.testing.assert_array_equal(s.cpu().numpy(), sr)
+    np.testing.assert_array_equal(q.cpu().numpy(), qr)
+    # Without the 1/127 floor: scales above and below the reciprocal form's lower limit.
+    tiny = np.array([1e-18, 3e-20, 1e-21, 1e-25, 2.0**-69, 2.0**-71], np.float64).astype(np.float32)
+    x = _near_half_integer_rows(rng, tiny, 1024)
+    q, s = quantize_rows_int8(dev(x), floor=False)
+    qr, sr = oracle.quantize_rows_int8(x, floor=False)
+    np.testing.assert_array_equal(s.cpu().numpy(), sr)
+    np.testing.assert_array_equal(q.cpu().numpy(), qr)
+
+
 def test_rows_int8_without_floor_is_labelled_non_reference() -> None:
     x = np.zeros((2, 32), np.float32)
     x[1] = np.float32(1e-4) * np.arange(32, dtype=np.float32)
