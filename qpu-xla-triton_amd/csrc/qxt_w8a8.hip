@@ -679,13 +679,19 @@ __device__ __forceinline__ void stage_rows(const GemmArgs &args, const FusedRows
             amax = fmaxf(fmaxf(scratch[0], scratch[1]), fmaxf(scratch[2], scratch[3]));
             __syncthreads();  // scratch is reused by the next row
             const float sc = row_scale(amax, f.floor != 0);
+            // Through the scale's reciprocal, as rows_int8_kernel.
+            const bool recip = sc >= kRecipScaleMin;
+            const float rc = recip ? 1.0f / sc : 0.0f;
+            auto quant = [&](uint32_t bits) {
+                const float x = __uint_as_float(bits);
+                return recip ? quant_recip(x, sc, rc) : quant_div(x, sc);
+            };
 #pragma unroll
             for (int u = 0; u < RC; ++u) {
                 const int c = threadIdx.x + u * kThreads;
                 if (c >= k4) break;
                 const v4u v = xv[u];
-                const uint32_t word = pack_bytes(quant_div(__uint_as_float(v[0]), sc), quant_div(__uint_as_float(v[1]), sc),
-                                                 quant_div(__uint_as_float(v[2]), sc), quant_div(__uint_as_float(v[3]), sc));
+                const uint32_t word = pack_bytes(quant(v[0]), quant(v[1]), quant(v[2]), quant(v[3]));
                 aw[r * k4 + c] = word;
                 if (blockIdx.x == 0)
                     reinterpret_cast<uint32_t *>(const_cast<int8_t *>(args.a) + static_cast<size_t>(r) * args.lda)[c] = word;
