@@ -856,6 +856,15 @@ constexpr int units_per_thread(int mr) { return mr == 1 ? 2 : 1; }
 #endif
 constexpr int kPrefetchUnits = QXT_PREFETCH_UNITS;
 
+#ifndef QXT_BALANCE_PREFETCH
+#define QXT_BALANCE_PREFETCH 1
+#endif
+constexpr bool kBalancePrefetchTiles = QXT_BALANCE_PREFETCH != 0;
+#ifndef QXT_BALANCE_MAXK
+#define QXT_BALANCE_MAXK 4
+#endif
+constexpr uint64_t kMaxBalancedPerCu = QXT_BALANCE_MAXK;
+
 // Whether one-row fp32 batches too large for the fused path (a whole decode
 // step) still quantise inside each workgroup, with the activation prefetch,
 // instead of running a pre-pass launch.
@@ -1277,6 +1286,32 @@ int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_
         natural = plan_items(upt, 1 << 30, nullptr, nullptr);
         if (natural < 0) return static_cast<int>(-natural);
         max_cpw = cap_for(natural);
+    }
+    if (prefetch_candidate && narrowed && kBalancePrefetchTiles) {
+        // Every CU the same number of workgroups: the narrowest tiles of
+        // kPrefetchUnits units per thread that give at most k workgroups per
+        // CU, for the smallest k that such tiles reach (a CU holding one
+        // workgroup more than the others sets the stage's time).  Measured
+        // on MI355X, the 88-launch staged decode step of cfg3: q/k/v 257 ->
+        // 235 workgroups and gate/up 352 -> 512, 0.428 -> 0.417 ms; two units
+        // per thread to reach one workgroup per CU on gate/up instead:
+        // 0.434 ms.
+        auto balanced = [&](uint64_t limit) -> int {
+            for (int c = static_cast<int>(std::max<uint64_t>(1, (columns + limit - 1) / limit));
+                 c <= kPrefetchUnits * kThreads; ++c) {
+                const int64_t n = plan_items(kPrefetchUnits, c, nullptr, nullptr);
+                if (n < 0) return 0;
+                if (static_cast<uint64_t>(n) <= limit) return c;
+            }
+            return 0;
+        };
+        for (uint64_t k = 1; k <= kMaxBalancedPerCu; ++k) {
+            const int c = balanced(k * static_cast<uint64_t>(compute_units()));
+            if (c > 0) {
+                max_cpw = c;
+                break;
+            }
+        }
     }
     size_t lds = 0;
     std::vector<Q4Item> items;
