@@ -301,20 +301,23 @@ __device__ __forceinline__ void stage_activation(const Q4Task &t, int r0, int *a
 }
 
 // Native Q8_0 activation rows of a four-row group for the matrix-core
-// tiles, requested into registers before any weight load: two (row, block)
-// items per thread (4 * blocks <= 512), 17 half-words each.  The loads are
-// unconditional (indexes clamped into the activation), so the compiler
-// counts the weight loads issued after them exactly and the staging waits
-// only for these.
+// tiles, requested into registers before any weight load: 512 / NT (row,
+// block) items per thread of an NT-thread workgroup (4 * blocks <= 512), 17
+// half-words each.  The loads are unconditional (indexes clamped into the
+// activation), so the compiler counts the weight loads issued after them
+// exactly and the staging waits only for these.
+template <int NT>
 struct Q8RowRegs {
-    uint32_t h[2][17];
+    static constexpr int kItems = 512 / NT;
+    uint32_t h[kItems][17];
 };
 
-__device__ __forceinline__ void fetch_q8_rows(const Q4Task &t, int r0, Q8RowRegs &a) {
+template <int NT>
+__device__ __forceinline__ void fetch_q8_rows(const Q4Task &t, int r0, Q8RowRegs<NT> &a) {
     const int B = t.blocks;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int idx = min(static_cast<int>(threadIdx.x) + i * kThreads, 4 * B - 1);
+    for (int i = 0; i < Q8RowRegs<NT>::kItems; ++i) {
+        const int idx = min(static_cast<int>(threadIdx.x) + i * NT, 4 * B - 1);
         const int r = idx / B;
         const int b = idx - r * B;
         const int row = min(r0 + r, t.rows - 1);
@@ -328,12 +331,13 @@ __device__ __forceinline__ void fetch_q8_rows(const Q4Task &t, int r0, Q8RowRegs
 // The LDS image of fetch_q8_rows' items, the records in the SCALES4 layout.
 // A row past t.rows holds a copy of the last row: a matrix-core output row
 // depends on its own activation row only, and those rows are never stored.
-__device__ __forceinline__ void stage_q8_rows(const Q4Task &t, const Q8RowRegs &a, int *aq, int *ad,
+template <int NT>
+__device__ __forceinline__ void stage_q8_rows(const Q4Task &t, const Q8RowRegs<NT> &a, int *aq, int *ad,
                                               const Q4Lds &geo) {
     const int B = t.blocks;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int idx = static_cast<int>(threadIdx.x) + i * kThreads;
+    for (int i = 0; i < Q8RowRegs<NT>::kItems; ++i) {
+        const int idx = static_cast<int>(threadIdx.x) + i * NT;
         if (idx >= 4 * B) break;
         const int r = idx / B;
         const int b = idx - r * B;
@@ -373,7 +377,7 @@ enum WeightLayout { kNativeRows = 0, kLaneLayout = 1, kEitherLayout = 2 };
 // load_units of the matrix-core tiles: units in mfma4_unit order, every
 // lane loading (CLAMP), G = 1 << lg.  Lane layout: one contiguous kilobyte
 // per wave instruction, non-temporal; native rows: each lane's 144 bytes.
-template <int U, int LAYOUT>
+template <int U, int LAYOUT, int NT>
 __device__ __forceinline__ void load_units_m4(const Q4Task &t, int col_base, int lg, int units, int first,
                                               uint32_t (&d)[U][36]) {
     const int lane = threadIdx.x & 63;
@@ -381,7 +385,7 @@ __device__ __forceinline__ void load_units_m4(const Q4Task &t, int col_base, int
     const int perm = ((((b >> lg) << 2) + p) << lg) + (b & ((1 << lg) - 1));
 #pragma unroll
     for (int j = 0; j < U; ++j) {
-        const int u = min(first + j * kThreads + (static_cast<int>(threadIdx.x) & ~63) + perm, units - 1);
+        const int u = min(first + j * NT + (static_cast<int>(threadIdx.x) & ~63) + perm, units - 1);
         const int col = u >> lg, g = u & ((1 << lg) - 1);
         if constexpr (LAYOUT == kLaneLayout) {
             const size_t unit = (static_cast<size_t>(t.wcol0 + col_base + col) << lg) + g;
@@ -612,7 +616,7 @@ __device__ __forceinline__ void compute_fast(const Q4Task &t, int col_base, int 
 // unsigned codes, the accumulator starting from -8 * sum(a) of each row (the
 // SCALES4 records), so every lane ends with the same exact signed dots as the
 // v_dot4 path and the block terms are the same bits.
-template <int U>
+template <int U, int NT>
 __device__ __forceinline__ void compute_mfma4(const Q4Task &t, int lg, int units, int first,
                                               const uint32_t (&wr)[U][36], const int *aq, const int *ad, float *cb,
                                               const Q4Lds &geo) {
@@ -623,7 +627,7 @@ __device__ __forceinline__ void compute_mfma4(const Q4Task &t, int lg, int units
     const int *arow = aq + p * geo.aq_row;
 #pragma unroll
     for (int j = 0; j < U; ++j) {
-        const int u = first + j * kThreads + (static_cast<int>(threadIdx.x) & ~63) + ((((b >> lg) << 2) + p) << lg) + g;
+        const int u = first + j * NT + (static_cast<int>(threadIdx.x) & ~63) + ((((b >> lg) << 2) + p) << lg) + g;
         const int col = u >> lg;
         float terms[4][8];
         auto do_block = [&](auto ic) {
@@ -674,11 +678,11 @@ __device__ __forceinline__ void compute_mfma4(const Q4Task &t, int lg, int units
 
 // Phase 3: one thread per (row, column) adds the column's block terms in
 // block order and stores the fp32 result.
-template <int MR, bool FAST>
+template <int MR, bool FAST, int NT = kThreads>
 __device__ __forceinline__ void sum_store(const Q4Task &t, int col_base, int r0, int tile_cols, const float *cb,
                                           const Q4Lds &geo) {
     const int B = t.blocks;
-    for (int k = threadIdx.x; k < MR * tile_cols; k += kThreads) {
+    for (int k = threadIdx.x; k < MR * tile_cols; k += NT) {
         const int r = k / tile_cols;
         const int col = k - r * tile_cols;
         if (r0 + r >= t.rows) continue;
@@ -701,10 +705,8 @@ __device__ __forceinline__ void sum_store(const Q4Task &t, int col_base, int r0,
 }
 
 // One linear: workgroup (x, y) owns columns [x * cpw, +cpw) and rows [y * MR, +MR).
-// MFMA4: four-row lane-layout tiles on the matrix cores (compute_mfma4).
-template <int MR, int U, bool FAST, bool DOTS, int LAYOUT = kNativeRows, bool MFMA4 = false>
+template <int MR, int U, bool FAST, bool DOTS, int LAYOUT = kNativeRows>
 __global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Task t) {
-    static_assert(!MFMA4 || (MR == 4 && FAST && !DOTS && LAYOUT != kEitherLayout), "matrix-core tiles: four rows");
     extern __shared__ int lds[];
     const int col_base = blockIdx.x * t.cpw;
     const int r0 = blockIdx.y * MR;
@@ -718,38 +720,6 @@ __global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Task t) {
     const int G = FAST ? (B >> 3) : B;
     const int units = tile_cols * G;
     uint32_t wr[FAST ? U : 1][36];
-
-    if constexpr (MFMA4) {
-        // The activation first, then two rounds of weights, so that the
-        // staging waits only for the activation and the weight stream runs
-        // through it.  The loads of every round are unconditional (lanes
-        // past the tile re-read its last unit), so the compiler counts them
-        // exactly in every wait.
-        Q8RowRegs a;
-        fetch_q8_rows(t, r0, a);
-        __builtin_amdgcn_sched_barrier(0);  // keep the activation loads first
-        uint32_t wn[U][36];
-        const int lg = __builtin_ctz(G);
-        load_units_m4<U, LAYOUT>(t, col_base, lg, units, 0, wr);
-        load_units_m4<U, LAYOUT>(t, col_base, lg, units, U * kThreads, wn);
-        __builtin_amdgcn_sched_barrier(0);
-        stage_q8_rows(t, a, aq, ad, geo);
-        __syncthreads();
-        // Two register sets in turn (no copies between them): each is
-        // refilled with the round after next as soon as it is computed.
-        constexpr int R = U * kThreads;
-        for (int first = 0;;) {
-            compute_mfma4<U>(t, lg, units, first, wr, aq, ad, cb, geo);
-            load_units_m4<U, LAYOUT>(t, col_base, lg, units, first + 2 * R, wr);
-            if ((first += R) >= units) break;
-            compute_mfma4<U>(t, lg, units, first, wn, aq, ad, cb, geo);
-            load_units_m4<U, LAYOUT>(t, col_base, lg, units, first + 2 * R, wn);
-            if ((first += R) >= units) break;
-        }
-        __syncthreads();
-        sum_store<MR, FAST>(t, col_base, r0, tile_cols, cb, geo);
-        return;
-    }
 
     if constexpr (FAST) load_units<U, LAYOUT>(t, col_base, G, units, 0, wr);
 
@@ -844,6 +814,59 @@ __global__ __launch_bounds__(kThreads) void q4_0_batch_kernel(const Q4Task *__re
     __syncthreads();
     sum_store<MR, true>(t, item.col_base, 0, item.ncols, cb, geo);
 }
+
+// The four-row matrix-core tiles (compute_mfma4): workgroup (x, y) of NT
+// threads owns columns [x * cpw, +cpw) and rows [4 y, +4), one unit per
+// thread and round.
+template <int LAYOUT, int NT>
+__global__ __launch_bounds__(NT) void q4_0_mfma4_kernel(Q4Task t) {
+    constexpr int MR = 4, U = 1;
+    extern __shared__ int lds[];
+    const int col_base = blockIdx.x * t.cpw;
+    const int r0 = blockIdx.y * MR;
+    const int B = t.blocks;
+    const Q4Lds geo(B, true);
+    int *aq = lds;                                                 // [MR][aq_row]
+    int *ad = aq + MR * geo.aq_row;                                // SCALES4 records
+    float *cb = reinterpret_cast<float *>(ad + MR * geo.ad_row);  // [MR][cpw][cbs]
+    const int tile_cols = min(t.cpw, t.ncols - col_base);
+    const int G = B >> 3;
+    const int units = tile_cols * G;
+    uint32_t wr[U][36];
+    // The activation first, then two rounds of weights, so that the
+    // staging waits only for the activation and the weight stream runs
+    // through it.  The loads of every round are unconditional (lanes
+    // past the tile re-read its last unit), so the compiler counts them
+    // exactly in every wait.
+    Q8RowRegs<NT> a;
+    fetch_q8_rows(t, r0, a);
+    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads first
+    uint32_t wn[U][36];
+    const int lg = __builtin_ctz(G);
+    load_units_m4<U, LAYOUT, NT>(t, col_base, lg, units, 0, wr);
+    load_units_m4<U, LAYOUT, NT>(t, col_base, lg, units, U * NT, wn);
+    __builtin_amdgcn_sched_barrier(0);
+    stage_q8_rows(t, a, aq, ad, geo);
+    __syncthreads();
+    // Two register sets in turn (no copies between them): each is
+    // refilled with the round after next as soon as it is computed.
+    constexpr int R = U * NT;
+    for (int first = 0;;) {
+        compute_mfma4<U, NT>(t, lg, units, first, wr, aq, ad, cb, geo);
+        load_units_m4<U, LAYOUT, NT>(t, col_base, lg, units, first + 2 * R, wr);
+        if ((first += R) >= units) break;
+        compute_mfma4<U, NT>(t, lg, units, first, wn, aq, ad, cb, geo);
+        load_units_m4<U, LAYOUT, NT>(t, col_base, lg, units, first + 2 * R, wn);
+        if ((first += R) >= units) break;
+    }
+    __syncthreads();
+    sum_store<MR, true, NT>(t, col_base, r0, tile_cols, cb, geo);
+}
+
+// Threads per matrix-core tile workgroup (measured on MI355X, cfg2 back to
+// back: 512 threads, two waves per SIMD, 11.2 / 6.8 us against 9.7 / 5.5 us
+// with 256 at N = 11008 / 4096).
+constexpr int kMfma4Threads = kThreads;
 
 // Units each thread owns per round on the fast path.
 constexpr int units_per_thread(int mr) { return mr == 1 ? 2 : 1; }
@@ -940,10 +963,10 @@ int launch_single(Q4Task t, hipStream_t stream) {
         const int G = t.blocks / 8;
         if constexpr (MR == 4)
             if (fast && t.x == nullptr && G <= 16 && 16 % G == 0)
-                return t.lanes ? launch(name, q4_0_linear_kernel<MR, U, true, false, kLaneLayout, true>, grid,
-                                        dim3(kThreads), lds, stream, t)
-                               : launch(name, q4_0_linear_kernel<MR, U, true, false, kNativeRows, true>, grid,
-                                        dim3(kThreads), lds, stream, t);
+                return t.lanes ? launch(name, q4_0_mfma4_kernel<kLaneLayout, kMfma4Threads>, grid,
+                                        dim3(kMfma4Threads), lds, stream, t)
+                               : launch(name, q4_0_mfma4_kernel<kNativeRows, kMfma4Threads>, grid,
+                                        dim3(kMfma4Threads), lds, stream, t);
         if (fast && t.lanes)
             return launch(name, q4_0_linear_kernel<MR, U, true, false, kLaneLayout>, grid, dim3(kThreads), lds, stream,
                           t);
