@@ -14,7 +14,8 @@ Also reported on the same JSON line:
                           per-launch device time (hipExtLaunchKernel events);
   * ``w8a8``          -- cfg4 dynamic-W8A8 prefill GEMMs (M=4096) in TOPS, whole
                           operator and GEMM-only, with an int8-MFMA roofline;
-  * ``configs``       -- cfg0 (rotated over >= 512 MB of weight copies), cfg1, cfg2;
+  * ``configs``       -- cfg0 (rotated over >= 512 MB of weight copies), cfg1, cfg2 (lane layout,
+                         and over the native ggml rows);
   * ``cpu_baseline``  -- the NumPy oracle of the reference CPU path on this host.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--legs decode,w8a8,gemv,prefill,geglu,shards,cfg0,cfg1,cfg2,copy,cpu]
@@ -444,8 +445,11 @@ def leg_decode(torch, args) -> dict:
     return result
 
 
-def leg_rotated_q4(torch, args, rows: int, k: int, n: int, seed: int) -> dict:
-    """One Q4_0 linear shape, cycling through >= 512 MB of distinct weight copies (lane layout)."""
+def leg_rotated_q4(torch, args, rows: int, k: int, n: int, seed: int, layout: str = "lanes") -> dict:
+    """One Q4_0 linear shape, cycling through >= 512 MB of distinct weight copies.
+
+    layout "lanes": the decode kernels' prepared lane layout; "native": the ggml rows as given.
+    """
     from qpu_xla_amd.kernels.ggml_q4_0 import pack_ggml_q4_0_lane_weights
     from qpu_xla_amd.kernels.quantize import quantize_q4_0, quantize_q8_0
 
@@ -459,14 +463,18 @@ def leg_rotated_q4(torch, args, rows: int, k: int, n: int, seed: int) -> dict:
     for _ in range(copies):
         w = torch.randn((n, k), generator=gen, device="cuda", dtype=torch.float32) * 0.02
         last_native = quantize_q4_0(w)  # kept for the output check of the last launch
-        weights.append(pack_ggml_q4_0_lane_weights(last_native))
+        weights.append(pack_ggml_q4_0_lane_weights(last_native) if layout == "lanes" else last_native)
         del w
     x = torch.randn((rows, k), generator=gen, device="cuda", dtype=torch.float32)
     xq = quantize_q8_0(x)
     y = torch.empty((rows, n), dtype=torch.float32, device="cuda")
     for lw in weights:
-        runner.add("qxt_ggml_q4_0_q8_0_linear_lanes", _p(xq), _rs(xq), _p(lw.packed), n, _p(y), _rs(y),
-                   rows, k // 32, 0, 0, n, runner.handle)
+        if layout == "lanes":
+            runner.add("qxt_ggml_q4_0_q8_0_linear_lanes", _p(xq), _rs(xq), _p(lw.packed), n, _p(y), _rs(y),
+                       rows, k // 32, 0, 0, n, runner.handle)
+        else:
+            runner.add("qxt_ggml_q4_0_q8_0_linear", _p(xq), _rs(xq), _p(lw), _rs(lw), _p(y), _rs(y),
+                       rows, k // 32, 0, 0, n, runner.handle)
     runner.run()
     torch.cuda.synchronize()
     times = runner.kernel_times(repeats=2)["q4_0_linear_kernel"]
@@ -476,7 +484,7 @@ def leg_rotated_q4(torch, args, rows: int, k: int, n: int, seed: int) -> dict:
     avg_ms = float(np.mean(times))
     out = {
         "shape": f"M={rows} K={k} N={n}",
-        "weight_layout": "lanes",
+        "weight_layout": layout,
         "copies": copies,
         "rotation_mb": copies * per / 1e6,
         "bytes_per_launch": b,
@@ -1050,6 +1058,9 @@ def main() -> int:
         out["cfg2"] = [leg_rotated_q4(torch, args, 4, 4096, 11008, 2), leg_rotated_q4(torch, args, 4, 4096, 4096, 2)]
         attach_floor(out["cfg2"][0], "cfg2_n11008")
         attach_floor(out["cfg2"][1], "cfg2_n4096")
+        # The same launches over the native ggml rows (the drop-in layout, no re-layout).
+        out["cfg2_native_layout"] = [leg_rotated_q4(torch, args, 4, 4096, 11008, 2, "native"),
+                                     leg_rotated_q4(torch, args, 4, 4096, 4096, 2, "native")]
         log(f"cfg2: {out['cfg2']}")
     if "w8a8" in legs:
         log("leg w8a8 (cfg4)")
@@ -1137,7 +1148,7 @@ def main() -> int:
         "shards": out.get("shards"),
         "w8a8_cpu_baseline": cpu_w8a8,
         "decode": decode,
-        "configs": {key: out[key] for key in ("cfg0", "cfg1", "cfg2") if key in out},
+        "configs": {key: out[key] for key in ("cfg0", "cfg1", "cfg2", "cfg2_native_layout") if key in out},
         "copy_ceiling_gbs": out.get("copy", {}).get("gbs"),
         "device": device,
     }
