@@ -170,7 +170,8 @@ int qxt_ggml_geglu_q8_0_split(const float *gate, size_t gate_row_stride, const f
  * wc = weight_column_start + j, for r < rows, j < column_count.
  * activation: Q8_0 u8 [rows, blocks, 34]; weight: Q4_0 u8 [>= wc+1, blocks, 18].
  * Writes only destination[:, output_column_start : +column_count].  rows >= 16 run on the
- * int8 matrix cores (one MFMA per 32 x 32 outputs and block), fewer rows on v_dot4.
+ * int8 matrix cores (one MFMA per 32 x 32 outputs and block); 4 to 15 rows with blocks / 8
+ * dividing 16 (K <= 4096) on v_mfma_i32_4x4x4_16b_i8; other shapes on v_dot4.
  * Replaces GGML_Q4_0_Q8_0_LINEAR_KERNEL (src/qpu_xla/kernels/ggml_q4_0.py:783-841)
  * and the device work of qpu_llama_q4_0_linear_submit (qpu_llama_q4_0.h:72-75). */
 int qxt_ggml_q4_0_q8_0_linear(const void *activation, size_t activation_row_stride,
