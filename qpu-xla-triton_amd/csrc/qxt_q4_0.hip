@@ -46,6 +46,7 @@
 // linear re-quantising the whole row -- measured 86-97 us per cfg3 step
 // against 79-81 us with the pre-pass.)
 #include <algorithm>
+#include <limits>
 #include <new>
 #include <type_traits>
 #include <utility>
@@ -790,19 +791,16 @@ __global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Task t) {
 // compile-time choice: under a run-time branch the compiler cannot count
 // the weight loads issued after it and waits for all of them.
 template <int MR, int U, int LAYOUT, int PC>
-__global__ __launch_bounds__(kThreads) void q4_0_batch_kernel(const Q4Task *__restrict__ tasks,
-                                                              const Q4Item *__restrict__ items) {
+__device__ __forceinline__ void batch_item(const Q4Task &t, int col_base, int ncols) {
     extern __shared__ int lds[];
-    const Q4Item item = items[blockIdx.x];
-    const Q4Task &t = tasks[item.task];
     const int B = t.blocks;
     const int G = B >> 3;
-    const int units = item.ncols * G;
+    const int units = ncols * G;
     static_assert(PC == 0 || MR == 1, "the activation prefetch serves one-row batches");
     float4 xv[PC > 0 ? PC : 1];
     if constexpr (PC > 0) prefetch_row<PC>(t, xv);
     uint32_t wr[U][36];
-    load_units<U, LAYOUT, (PC > 0)>(t, item.col_base, G, units, 0, wr);
+    load_units<U, LAYOUT, (PC > 0)>(t, col_base, G, units, 0, wr);
     const Q4Lds geo(B, true);
     int *aq = lds;
     int *ad = aq + MR * geo.aq_row;
@@ -810,9 +808,39 @@ __global__ __launch_bounds__(kThreads) void q4_0_batch_kernel(const Q4Task *__re
     if constexpr (PC > 0) quantise_row<PC>(t, xv, aq, ad, geo);
     else stage_activation<MR>(t, 0, aq, ad, geo);
     __syncthreads();
-    compute_fast<MR, U, false>(t, item.col_base, 0, G, units, 0, wr, aq, ad, cb, geo);
+    compute_fast<MR, U, false>(t, col_base, 0, G, units, 0, wr, aq, ad, cb, geo);
     __syncthreads();
-    sum_store<MR, true>(t, item.col_base, 0, item.ncols, cb, geo);
+    sum_store<MR, true>(t, col_base, 0, ncols, cb, geo);
+}
+
+template <int MR, int U, int LAYOUT, int PC>
+__global__ __launch_bounds__(kThreads) void q4_0_batch_kernel(const Q4Task *__restrict__ tasks,
+                                                              const Q4Item *__restrict__ items) {
+    const Q4Item item = items[blockIdx.x];
+    batch_item<MR, U, LAYOUT, PC>(tasks[item.task], item.col_base, item.ncols);
+}
+
+// A batch of at most kArgTasks tasks travels in the kernel arguments: each
+// workgroup finds its task and column tile from its index, without the two
+// dependent reads of a device table (item, then task) before its first
+// weight or activation request.  Task j's items start at first_item[j]
+// (INT_MAX past the last task) and are its column tiles of cpw columns in
+// order.
+constexpr int kArgTasks = 4;
+struct Q4ArgBatch {
+    int first_item[kArgTasks];
+    Q4Task task[kArgTasks];
+};
+
+template <int MR, int U, int LAYOUT, int PC>
+__global__ __launch_bounds__(kThreads) void q4_0_arg_batch_kernel(Q4ArgBatch a) {
+    const int i = static_cast<int>(blockIdx.x);
+    int ti = 0;
+#pragma unroll
+    for (int j = 1; j < kArgTasks; ++j) ti += i >= a.first_item[j] ? 1 : 0;
+    const Q4Task t = a.task[ti];
+    const int col_base = (i - a.first_item[ti]) * t.cpw;
+    batch_item<MR, U, LAYOUT, PC>(t, col_base, min(t.cpw, t.ncols - col_base));
 }
 
 // The four-row matrix-core tiles (compute_mfma4): workgroup (x, y) of NT
@@ -895,6 +923,11 @@ constexpr uint64_t kMaxBalancedPerCu = QXT_BALANCE_MAXK;
 #define QXT_PREFETCH_LARGE 0
 #endif
 constexpr bool kPrefetchLargeBatches = QXT_PREFETCH_LARGE != 0;
+
+#ifndef QXT_ARG_BATCH
+#define QXT_ARG_BATCH 1
+#endif
+constexpr bool kArgBatches = QXT_ARG_BATCH != 0;
 
 static_assert(kPrefetchUnits >= 1 && kPrefetchUnits <= units_per_thread(1),
               "a prefetch plan must fit the one-row batch kernel it falls back to");
@@ -1036,18 +1069,30 @@ struct qxt_q4_0_batch {
     int prefetch = 0;  // activation chunks per thread prefetched (every task one fp32 row), or 0
     int upt = 1;       // units per thread of the batch kernel
     size_t lds = 0;
+    bool in_args = false;  // tasks and items travel in the kernel arguments
+    Q4ArgBatch args{};
 };
 
 namespace qxt {
 namespace {
 
-using BatchKernel = void (*)(const Q4Task *, const Q4Item *);
+// The two forms of one batch kernel: tasks and items in device tables, or
+// (at most kArgTasks tasks) in the kernel arguments.
+struct BatchKernel {
+    void (*tables)(const Q4Task *, const Q4Item *);
+    void (*args)(Q4ArgBatch);
+};
+
+template <int MR, int U, int LAYOUT, int PC>
+BatchKernel batch_kernels() {
+    return {q4_0_batch_kernel<MR, U, LAYOUT, PC>, q4_0_arg_batch_kernel<MR, U, LAYOUT, PC>};
+}
 
 template <int MR, int U, int PC>
 BatchKernel batch_kernel_for(int layout) {
-    return layout == kLaneLayout    ? q4_0_batch_kernel<MR, U, kLaneLayout, PC>
-           : layout == kNativeRows ? q4_0_batch_kernel<MR, U, kNativeRows, PC>
-                                   : q4_0_batch_kernel<MR, U, kEitherLayout, PC>;
+    return layout == kLaneLayout    ? batch_kernels<MR, U, kLaneLayout, PC>()
+           : layout == kNativeRows ? batch_kernels<MR, U, kNativeRows, PC>()
+                                   : batch_kernels<MR, U, kEitherLayout, PC>();
 }
 
 template <int U>
@@ -1407,6 +1452,16 @@ int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_
     if (prefetch_candidate)
         for (const Q4Task &t : host) batch->prefetch = std::max(batch->prefetch, prefetch_chunks(t));
     batch->lds = lds;
+    if (kArgBatches && count <= static_cast<uint32_t>(kArgTasks)) {
+        batch->in_args = true;
+        for (int j = 0; j < kArgTasks; ++j) batch->args.first_item[j] = std::numeric_limits<int>::max();
+        int first = 0;
+        for (uint32_t i = 0; i < count; ++i) {
+            batch->args.task[i] = host[i];
+            batch->args.first_item[i] = first;
+            first += (host[i].ncols + host[i].cpw - 1) / host[i].cpw;
+        }
+    }
     *out = batch;
     return QXT_OK;
 }
@@ -1420,8 +1475,11 @@ int qxt_q4_0_batch_launch(const qxt_q4_0_batch *batch, void *stream) {
                     as_stream(stream), batch->jobs, batch->chunks);
         if (rc != QXT_OK) return rc;
     }
-    return launch("q4_0_batch_kernel", batch_kernel(batch->mr, batch->layout, batch->prefetch, batch->upt), dim3(batch->grid), dim3(kThreads),
-                  batch->lds,
+    const BatchKernel kernel = batch_kernel(batch->mr, batch->layout, batch->prefetch, batch->upt);
+    if (batch->in_args)
+        return launch("q4_0_batch_kernel", kernel.args, dim3(batch->grid), dim3(kThreads), batch->lds,
+                      as_stream(stream), batch->args);
+    return launch("q4_0_batch_kernel", kernel.tables, dim3(batch->grid), dim3(kThreads), batch->lds,
                   as_stream(stream), batch->tasks, batch->items);
 }
 

@@ -243,6 +243,34 @@ def test_batch_many_work_items_eager_and_graph_replays() -> None:
         del graph
 
 
+@pytest.mark.parametrize("count", [1, 4, 5])
+def test_batch_in_kernel_arguments_and_in_device_tables_bit_exact(count: int) -> None:
+    # Up to four tasks travel in the kernel arguments (each workgroup finds its
+    # task and column tile from its index), more in device tables.  Either
+    # form, launched eagerly and replayed from a captured graph, matches the
+    # oracle; ragged tiles end every task.
+    shapes = [(1, 2048, 700, 0, 700), (1, 5632, 300, 4, 290), (1, 256, 64, 0, 64), (1, 4096, 96, 16, 77),
+              (1, 2048, 130, 0, 130)][:count]
+    tasks, expected = _batch_case(60 + count, shapes, fused_every=1)
+    stream = torch.cuda.Stream()
+    with q4.Q4_0LinearBatch(tasks) as batch:
+        assert batch.task_count == count and batch.work_items >= count
+        batch.launch(stream)
+        stream.synchronize()
+        _check_batch(tasks, expected)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            batch.launch(stream)
+        for _ in range(2):
+            for t in tasks:
+                t["destination"][:, 16:] = -1.0
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            _check_batch(tasks, expected)
+        del graph
+
+
 def test_batch_small_m_bit_exact() -> None:
     shapes = [(4, 4096, 64, 0, 64), (2, 2048, 40, 8, 32), (3, 256, 16, 0, 16), (1, 512, 33, 0, 33)]
     tasks, expected = _batch_case(32, shapes, fused_every=3)
