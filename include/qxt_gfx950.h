@@ -120,6 +120,14 @@ int qxt_timing_end(qxt_launch_record *records, uint32_t capacity, uint32_t *coun
 int qxt_quantize_q8_0(const float *x, size_t x_row_stride, void *blocks, size_t blocks_row_stride,
                       uint32_t rows, uint32_t columns, void *stream);
 
+/* Self-check with no reference counterpart, for test suites: compares the
+ * Q8_0 block scale d and inverse inv that the Q8_0 quantisers compute without
+ * division sequences against fl32(absmax/127) and fl32(1/d) from IEEE
+ * division, for every non-negative fp32 absmax (all 2^31 bit patterns), and
+ * adds the number of patterns that differ to *mismatches, a device uint64
+ * the caller zeroes. */
+int qxt_q8_0_scale_check(uint64_t *mismatches, void *stream);
+
 /* fp32 rows x[rows, columns] -> int8 q[rows, padded_columns] plus fp32 scales[rows].
  * scale = max(fl32(absmax/127), fl32(1/127)), q = clip(rint(x/scale), +-127);
  * columns [columns, padded_columns) are written as 0.  Replaces the host

@@ -141,6 +141,37 @@ __device__ __forceinline__ int quant_recip(float v, float s, float r) {
     return clamp127(rintf(fmaf(e, r, q0)));
 }
 
+// The Q8_0 block scale d = fl(amax / 127) and inv = fl(1 / d) (0 when d is
+// 0) -- the two IEEE divisions of the rule -- without the division
+// sequences.  d: q0 = fl(amax r) with r = fl(1/127) is within an ulp of the
+// quotient, the residual fma(-q0, 127, amax) is exact and fma(residual, r,
+// q0) is the correctly rounded quotient (Markstein's theorem).  inv: the
+// hardware reciprocal y0 of d, then one fused Newton step fma(fma(-d, y0, 1),
+// y0, y0).  amax outside [2^-96, 2^120] (zero, tiny, huge, inf or NaN)
+// divides.  Both results equal the IEEE divisions for every non-negative
+// fp32 amax: qxt_q8_0_scale_check compares them over all 2^31 bit patterns
+// on the device.
+constexpr float kQ8FastScaleMin = 0x1p-96f, kQ8FastScaleMax = 0x1p120f;
+__device__ __forceinline__ bool q8_0_fast_scale_range(float amax) {
+    return amax >= kQ8FastScaleMin && amax <= kQ8FastScaleMax;  // false for NaN
+}
+// The division-free sequence alone: correct only where q8_0_fast_scale_range.
+__device__ __forceinline__ void q8_0_scale_fast(float amax, float &d, float &inv) {
+    const float r = static_cast<float>(1.0 / 127.0);
+    const float q0 = amax * r;
+    d = fmaf(fmaf(-q0, 127.0f, amax), r, q0);
+    const float y0 = __builtin_amdgcn_rcpf(d);
+    inv = fmaf(fmaf(-d, y0, 1.0f), y0, y0);
+}
+__device__ __forceinline__ void q8_0_scale(float amax, float &d, float &inv) {
+    if (q8_0_fast_scale_range(amax)) {
+        q8_0_scale_fast(amax, d, inv);
+    } else {
+        d = amax / 127.0f;
+        inv = d != 0.0f ? 1.0f / d : 0.0f;
+    }
+}
+
 __device__ __forceinline__ uint32_t pack_bytes(int q0, int q1, int q2, int q3) {
     return (static_cast<uint32_t>(q0) & 0xFFu) | ((static_cast<uint32_t>(q1) & 0xFFu) << 8) |
            ((static_cast<uint32_t>(q2) & 0xFFu) << 16) | ((static_cast<uint32_t>(q3) & 0xFFu) << 24);

@@ -70,8 +70,8 @@ __global__ __launch_bounds__(kThreads) void q8_0_kernel(const float *__restrict_
     const float4 v = load4<VEC>(src);
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     amax = group8_max(amax);
-    const float d = amax / 127.0f;
-    const float inv = (d != 0.0f) ? 1.0f / d : 0.0f;
+    float d, inv;
+    q8_0_scale(amax, d, inv);
     const int q0 = clamp127(rintf(v.x * inv));
     const int q1 = clamp127(rintf(v.y * inv));
     const int q2 = clamp127(rintf(v.z * inv));
@@ -167,8 +167,8 @@ __device__ __forceinline__ void geglu_blocks(uint64_t first, uint64_t stride, ui
         const float v3 = half_bits_to_float(lookup(float_to_half_bits(g[i].w))) * u[i].w;
         float amax = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
         amax = group8_max(amax);
-        const float d = amax / 127.0f;
-        const float inv = (d != 0.0f) ? 1.0f / d : 0.0f;
+        float d, inv;
+        q8_0_scale(amax, d, inv);
         const uint32_t word = pack_bytes(clamp127(rintf(v0 * inv)), clamp127(rintf(v1 * inv)),
                                          clamp127(rintf(v2 * inv)), clamp127(rintf(v3 * inv)));
         const uint32_t d_bits = float_to_half_bits(d);
@@ -424,12 +424,40 @@ int launch_geglu(const float *gate, size_t gate_stride, const float *up, size_t 
                   blocks);
 }
 
+// q8_0_scale against the two IEEE divisions it replaces, for every
+// non-negative fp32 amax (all 2^31 bit patterns, grid-stride): adds the
+// number of patterns whose d or inv differs (NaN matches NaN) to *mismatches.
+__global__ __launch_bounds__(kThreads) void q8_0_scale_check_kernel(unsigned long long *mismatches) {
+    const uint32_t stride = gridDim.x * kThreads;
+    unsigned int bad = 0;
+    for (uint32_t bits = blockIdx.x * kThreads + threadIdx.x; bits < 0x80000000u; bits += stride) {
+        const float amax = __uint_as_float(bits);
+        float d, inv;
+        q8_0_scale(amax, d, inv);
+        const float dr = amax / 127.0f;
+        const float ir = dr != 0.0f ? 1.0f / dr : 0.0f;
+        const bool d_ok = __float_as_uint(d) == __float_as_uint(dr) || (d != d && dr != dr);
+        const bool i_ok = __float_as_uint(inv) == __float_as_uint(ir) || (inv != inv && ir != ir);
+        bad += (d_ok && i_ok) ? 0u : 1u;
+        if (stride > 0x80000000u - bits) break;  // the next pattern would pass 2^31 (no wrap)
+    }
+    if (bad != 0) atomicAdd(mismatches, static_cast<unsigned long long>(bad));
+}
+
 }  // namespace
 }  // namespace qxt
 
 using namespace qxt;
 
 extern "C" {
+
+int qxt_q8_0_scale_check(uint64_t *mismatches, void *stream) {
+    if (mismatches == nullptr || !aligned(mismatches, 8)) return fail(QXT_INVALID_ARGUMENT, "q8_0 scale check: bad counter");
+    int rc = injected(QXT_FAIL_SUBMISSION);
+    if (rc != QXT_OK) return rc;
+    return launch("q8_0_scale_check_kernel", q8_0_scale_check_kernel, dim3(8192), dim3(kThreads), 0,
+                  as_stream(stream), reinterpret_cast<unsigned long long *>(mismatches));
+}
 
 int qxt_quantize_q8_0(const float *x, size_t x_row_stride, void *blocks, size_t blocks_row_stride,
                       uint32_t rows, uint32_t columns, void *stream) {

@@ -271,6 +271,33 @@ def test_batch_in_kernel_arguments_and_in_device_tables_bit_exact(count: int) ->
         del graph
 
 
+@pytest.mark.parametrize("k", [2048, 5632])
+def test_stage_batch_activation_blocks_outside_the_fast_scale_range_bit_exact(k: int) -> None:
+    # The prefetching stage kernels quantise their fp32 row with the
+    # division-free Q8_0 scale and quantise a thread's chunks again with
+    # divisions when one of its blocks has absmax outside [2^-96, 2^120]:
+    # zero blocks, tiny blocks, blocks on the range's edges, next to ordinary
+    # ones, through both weight layouts.
+    rng = np.random.default_rng(k)
+    x = rng.standard_normal((1, k), dtype=np.float32)
+    blocks = x.reshape(1, k // 32, 32)
+    for b, scale in [(0, 0.0), (3, 2.0**-100), (5, 2.0**-96), (8, 2.0**-97), (13, 2.0**-95), (21, 2.0**-110),
+                     (34, 2.0**-120), (55, 0.0)]:
+        blocks[0, b] *= np.float32(scale)
+    n = 300
+    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    wq = oracle.quantize_q4_0_blocks(w)
+    want = oracle.q4_0_q8_0_reference(oracle.quantize_q8_0_blocks(x), wq)
+    for weight in (dev(wq), q4.pack_ggml_q4_0_lane_weights(dev(wq))):
+        dest = torch.full((1, n + 16), float(SENTINEL), device="cuda")
+        tasks = [{"x": dev(x), "weight": weight, "destination": dest, "weight_column_start": 0,
+                  "output_column_start": 16, "column_count": n}]
+        with q4.Q4_0LinearBatch(tasks) as batch:
+            batch.launch()
+            torch.cuda.synchronize()
+        _check_batch(tasks, [want])
+
+
 def test_batch_small_m_bit_exact() -> None:
     shapes = [(4, 4096, 64, 0, 64), (2, 2048, 40, 8, 32), (3, 256, 16, 0, 16), (1, 512, 33, 0, 33)]
     tasks, expected = _batch_case(32, shapes, fused_every=3)

@@ -2,6 +2,8 @@
 
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -25,6 +27,39 @@ def test_fixture_vectors() -> None:
     np.testing.assert_array_equal(q.cpu().numpy(), g["rows_q"])
     np.testing.assert_array_equal(s.cpu().numpy(), g["rows_scale"])
     np.testing.assert_array_equal(quantize_q4_0(dev(g["w"])).cpu().numpy(), g["q4_0_blocks"])
+
+
+def test_q8_0_scale_without_division_equals_ieee_division_for_every_absmax() -> None:
+    # The Q8_0 quantisers compute d = fl32(absmax / 127) and inv = fl32(1 / d)
+    # without division sequences; the device compares both with IEEE division
+    # for all 2^31 non-negative fp32 bit patterns (zero, subnormals, the fast
+    # range's edges, inf and NaN included).
+    from qpu_xla_amd import _lib
+
+    counter = torch.zeros(1, dtype=torch.int64, device="cuda")
+    _lib.call("qxt_q8_0_scale_check", ctypes.c_void_p(counter.data_ptr()), None)
+    torch.cuda.synchronize()
+    assert int(counter.item()) == 0
+
+
+def test_q8_0_blocks_at_the_edges_of_the_fast_scale_range_bit_exact() -> None:
+    # Blocks whose absmax sits at, just inside and just outside [2^-96, 2^120]
+    # (outside, the quantisers divide) and at all-ones significands: the codes
+    # and fp16 scales equal the oracle's, which divides.  (Smaller maxima give
+    # subnormal scales whose reciprocal overflows; the scale check above covers
+    # them.)
+    edges = [2.0**-96, 2.0**120, np.nextafter(np.float32(2.0**-96), np.float32(0)),
+             np.nextafter(np.float32(2.0**120), np.float32(np.inf)), np.float32(2.0**-96) * np.float32(1.9999999),
+             np.float32(2.0**119) * np.float32(1.9999999), np.float32(1.9999999), np.float32(127.0),
+             np.float32(2.0**-90) * np.float32(1.5), np.float32(65504.0) * np.float32(127.0)]
+    rng = np.random.default_rng(77)
+    x = np.empty((len(edges), 64), dtype=np.float32)
+    for i, e in enumerate(edges):
+        block = (rng.uniform(-1.0, 1.0, 64) * np.float32(e)).astype(np.float32)
+        block[rng.integers(0, 32)] = np.float32(e) * (1 if i % 2 else -1)
+        block[32 + rng.integers(0, 32)] = np.float32(e)
+        x[i] = block
+    np.testing.assert_array_equal(quantize_q8_0(dev(x)).cpu().numpy(), oracle.quantize_q8_0_blocks(x))
 
 
 @pytest.mark.parametrize("rows,cols", [(1, 32), (3, 96), (7, 2048), (64, 5632), (2, 14336)])
