@@ -810,6 +810,138 @@ __global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Task t) {
 // K <= 256 * 4 * PC): the activation row is requested before the weights.  A
 // compile-time choice: under a run-time branch the compiler cannot count
 // the weight loads issued after it and waits for all of them.
+//
+// S > 1 (one-row prefetch batches of at most 64 * 4 / S units per item):
+// each unit is split over S waves.  Wave w takes part w % S -- blocks
+// [8/S * part, +8/S) -- of units 64 * (w / S) + lane, loading only the
+// 16-byte chunks that hold them, so each wave's share of the block dots is
+// 1/S of a unit instead of a whole unit on fewer lanes.
+
+// Part P (of S) of a unit: blocks [8/S * P, +8/S), which lie in 16-byte
+// chunks [2P, 2P + 2] (S = 4) or [4P, 4P + 4] (S = 2) -- block i of a
+// 144-byte unit spans bytes 18 i .. 18 i + 17.
+template <int S>
+struct UnitParts {
+    static constexpr int kBlocks = 8 / S;
+    static constexpr int kChunks = S == 4 ? 3 : 5;
+    static constexpr int kChunkStep = S == 4 ? 2 : 4;  // first chunk of part P = kChunkStep * P
+    static_assert((18 * kBlocks * (S - 1) + 18 * kBlocks - 1) / 16 == kChunkStep * (S - 1) + kChunks - 1,
+                  "the last part's chunks end with the unit");
+};
+
+// The chunks of this wave's part (first chunk c0, the same for the whole
+// wave) of unit u: one code path for every part, so every wave issues the
+// same loads and the waits that follow count them exactly.
+template <int S, int LAYOUT>
+__device__ __forceinline__ void load_part(const Q4Task &t, int col_base, int G, int units, int u, int c0,
+                                          uint32_t (&d)[4 * UnitParts<S>::kChunks]) {
+    const int uc = min(u, units - 1);  // unconditional: lanes past the tile re-read its last unit
+    const int col = uc / G;
+    const int g = uc - col * G;
+    if (LAYOUT == kLaneLayout || (LAYOUT == kEitherLayout && t.lanes)) {
+        const size_t unit = static_cast<size_t>(t.wcol0 + col_base + col) * G + g;
+        const QXT_GLOBAL v4u *src = global_in<v4u>(t.w + (unit / kLaneGroup) * kGroupBytes + (unit % kLaneGroup) * 16) +
+                                    c0 * kLaneGroup;
+#pragma unroll
+        for (int v = 0; v < UnitParts<S>::kChunks; ++v) {
+            const v4u x = __builtin_nontemporal_load(src + v * kLaneGroup);
+            d[4 * v + 0] = x[0];
+            d[4 * v + 1] = x[1];
+            d[4 * v + 2] = x[2];
+            d[4 * v + 3] = x[3];
+        }
+    } else {
+        const QXT_GLOBAL v4u *src = global_in<v4u>(t.w + static_cast<size_t>(t.wcol0 + col_base + col) * t.w_stride +
+                                                   static_cast<size_t>(g) * 144) +
+                                    c0;
+#pragma unroll
+        for (int v = 0; v < UnitParts<S>::kChunks; ++v) {
+            const v4u x = src[v];
+            d[4 * v + 0] = x[0];
+            d[4 * v + 1] = x[1];
+            d[4 * v + 2] = x[2];
+            d[4 * v + 3] = x[3];
+        }
+    }
+}
+
+// Block terms of part P of unit u (one row) into cb; `pr` holds the part's
+// chunks as load_part left them.
+template <int S, int P>
+__device__ __forceinline__ void compute_part(int G, int units, int u, const uint32_t (&pr)[4 * UnitParts<S>::kChunks],
+                                             const int *aq, const int *ad, float *cb, const Q4Lds &geo) {
+    using Parts = UnitParts<S>;
+    constexpr int NB = Parts::kBlocks, I0 = NB * P, W0 = 4 * Parts::kChunkStep * P;
+    if (u >= units) return;
+    // The unit's words at their places in a whole unit (register renaming only).
+    uint32_t d[36];
+#pragma unroll
+    for (int k = 0; k < 4 * Parts::kChunks; ++k) d[W0 + k] = pr[k];
+    const int col = u / G;
+    const int g = u - col * G;
+    int4 lo[NB], hi[NB];
+    int2 ds[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const int b = g * 8 + I0 + i;
+        lo[i] = *reinterpret_cast<const int4 *>(aq + aq_index(b, 0));
+        hi[i] = *reinterpret_cast<const int4 *>(aq + aq_index(b, 4));
+        ds[i] = *reinterpret_cast<const int2 *>(ad + ad_index(b));
+    }
+    float terms[NB];
+    auto do_block = [&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        uint32_t sbits, qs[4];
+        unit_block<I0 + i>(d, sbits, qs);
+        const float v = static_cast<float>(block_dot(qs, lo[i], hi[i], ds[i].y)) * half_bits_to_float(sbits);
+        terms[i] = v * __int_as_float(ds[i].x);
+    };
+    do_block(std::integral_constant<int, 0>{});
+    do_block(std::integral_constant<int, 1>{});
+    if constexpr (NB == 4) {
+        do_block(std::integral_constant<int, 2>{});
+        do_block(std::integral_constant<int, 3>{});
+    }
+    float *dst = cb + col * geo.cbs + g * 8 + I0;
+    if constexpr (NB == 4) *reinterpret_cast<float4 *>(dst) = make_float4(terms[0], terms[1], terms[2], terms[3]);
+    else *reinterpret_cast<float2 *>(dst) = make_float2(terms[0], terms[1]);
+}
+
+template <int LAYOUT, int PC, int S>
+__device__ __forceinline__ void batch_item_split(const Q4Task &t, int col_base, int ncols) {
+    static_assert(S == 2 || S == 4, "a unit splits into 2 or 4 parts");
+    extern __shared__ int lds[];
+    const int B = t.blocks;
+    const int G = B >> 3;
+    const int units = ncols * G;
+    float4 xv[PC];
+    prefetch_row<PC>(t, xv);
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int part = wave % S;
+    const int u = (wave / S) * 64 + static_cast<int>(threadIdx.x & 63);
+    uint32_t pr[4 * UnitParts<S>::kChunks];
+    load_part<S, LAYOUT>(t, col_base, G, units, u, UnitParts<S>::kChunkStep * part, pr);
+    const Q4Lds geo(B, true);
+    int *aq = lds;
+    int *ad = aq + geo.aq_row;
+    float *cb = reinterpret_cast<float *>(ad + geo.ad_row);
+    quantise_row<PC>(t, xv, aq, ad, geo);
+    __syncthreads();
+    if constexpr (S == 2) {
+        if (part == 0) compute_part<2, 0>(G, units, u, pr, aq, ad, cb, geo);
+        else compute_part<2, 1>(G, units, u, pr, aq, ad, cb, geo);
+    } else {
+        switch (part) {
+            case 0: compute_part<4, 0>(G, units, u, pr, aq, ad, cb, geo); break;
+            case 1: compute_part<4, 1>(G, units, u, pr, aq, ad, cb, geo); break;
+            case 2: compute_part<4, 2>(G, units, u, pr, aq, ad, cb, geo); break;
+            default: compute_part<4, 3>(G, units, u, pr, aq, ad, cb, geo); break;
+        }
+    }
+    __syncthreads();
+    sum_store<1, true>(t, col_base, 0, ncols, cb, geo);
+}
+
 template <int MR, int U, int LAYOUT, int PC>
 __device__ __forceinline__ void batch_item(const Q4Task &t, int col_base, int ncols) {
     extern __shared__ int lds[];
@@ -833,11 +965,17 @@ __device__ __forceinline__ void batch_item(const Q4Task &t, int col_base, int nc
     sum_store<MR, true>(t, col_base, 0, ncols, cb, geo);
 }
 
-template <int MR, int U, int LAYOUT, int PC>
+template <int MR, int U, int LAYOUT, int PC, int S = 1>
+__device__ __forceinline__ void batch_item_any(const Q4Task &t, int col_base, int ncols) {
+    if constexpr (S > 1) batch_item_split<LAYOUT, PC, S>(t, col_base, ncols);
+    else batch_item<MR, U, LAYOUT, PC>(t, col_base, ncols);
+}
+
+template <int MR, int U, int LAYOUT, int PC, int S = 1>
 __global__ __launch_bounds__(kThreads) void q4_0_batch_kernel(const Q4Task *__restrict__ tasks,
                                                               const Q4Item *__restrict__ items) {
     const Q4Item item = items[blockIdx.x];
-    batch_item<MR, U, LAYOUT, PC>(tasks[item.task], item.col_base, item.ncols);
+    batch_item_any<MR, U, LAYOUT, PC, S>(tasks[item.task], item.col_base, item.ncols);
 }
 
 // A batch of at most kArgTasks tasks travels in the kernel arguments: each
@@ -852,7 +990,7 @@ struct Q4ArgBatch {
     Q4Task task[kArgTasks];
 };
 
-template <int MR, int U, int LAYOUT, int PC>
+template <int MR, int U, int LAYOUT, int PC, int S = 1>
 __global__ __launch_bounds__(kThreads) void q4_0_arg_batch_kernel(Q4ArgBatch a) {
     const int i = static_cast<int>(blockIdx.x);
     int ti = 0;
@@ -860,7 +998,7 @@ __global__ __launch_bounds__(kThreads) void q4_0_arg_batch_kernel(Q4ArgBatch a) 
     for (int j = 1; j < kArgTasks; ++j) ti += i >= a.first_item[j] ? 1 : 0;
     const Q4Task t = a.task[ti];
     const int col_base = (i - a.first_item[ti]) * t.cpw;
-    batch_item<MR, U, LAYOUT, PC>(t, col_base, min(t.cpw, t.ncols - col_base));
+    batch_item_any<MR, U, LAYOUT, PC, S>(t, col_base, min(t.cpw, t.ncols - col_base));
 }
 
 // The four-row matrix-core tiles (compute_mfma4): workgroup (x, y) of NT
@@ -943,6 +1081,11 @@ constexpr uint64_t kMaxBalancedPerCu = QXT_BALANCE_MAXK;
 #define QXT_PREFETCH_LARGE 0
 #endif
 constexpr bool kPrefetchLargeBatches = QXT_PREFETCH_LARGE != 0;
+
+#ifndef QXT_SPLIT_UNITS
+#define QXT_SPLIT_UNITS 1
+#endif
+constexpr bool kSplitUnits = QXT_SPLIT_UNITS != 0;
 
 #ifndef QXT_ARG_BATCH
 #define QXT_ARG_BATCH 1
@@ -1088,6 +1231,7 @@ struct qxt_q4_0_batch {
     int layout = 0;  // WeightLayout of every task (kEitherLayout when mixed)
     int prefetch = 0;  // activation chunks per thread prefetched (every task one fp32 row), or 0
     int upt = 1;       // units per thread of the batch kernel
+    int split = 1;     // waves per unit (one-row prefetch batches of narrow items)
     size_t lds = 0;
     bool in_args = false;  // tasks and items travel in the kernel arguments
     Q4ArgBatch args{};
@@ -1103,33 +1247,44 @@ struct BatchKernel {
     void (*args)(Q4ArgBatch);
 };
 
-template <int MR, int U, int LAYOUT, int PC>
+template <int MR, int U, int LAYOUT, int PC, int S>
 BatchKernel batch_kernels() {
-    return {q4_0_batch_kernel<MR, U, LAYOUT, PC>, q4_0_arg_batch_kernel<MR, U, LAYOUT, PC>};
+    return {q4_0_batch_kernel<MR, U, LAYOUT, PC, S>, q4_0_arg_batch_kernel<MR, U, LAYOUT, PC, S>};
 }
 
-template <int MR, int U, int PC>
+template <int MR, int U, int PC, int S = 1>
 BatchKernel batch_kernel_for(int layout) {
-    return layout == kLaneLayout    ? batch_kernels<MR, U, kLaneLayout, PC>()
-           : layout == kNativeRows ? batch_kernels<MR, U, kNativeRows, PC>()
-                                   : batch_kernels<MR, U, kEitherLayout, PC>();
+    return layout == kLaneLayout    ? batch_kernels<MR, U, kLaneLayout, PC, S>()
+           : layout == kNativeRows ? batch_kernels<MR, U, kNativeRows, PC, S>()
+                                   : batch_kernels<MR, U, kEitherLayout, PC, S>();
+}
+
+template <int U, int PC>
+BatchKernel prefetch_kernel_split(int layout, int split) {
+    if constexpr (U == 1) {
+        if (split == 4) return batch_kernel_for<1, 1, PC, 4>(layout);
+        if (split == 2) return batch_kernel_for<1, 1, PC, 2>(layout);
+    }
+    return batch_kernel_for<1, U, PC>(layout);
 }
 
 template <int U>
-BatchKernel prefetch_kernel(int layout, int prefetch) {
+BatchKernel prefetch_kernel(int layout, int prefetch, int split) {
     switch (prefetch) {
-        case 2: return batch_kernel_for<1, U, 2>(layout);
-        case 4: return batch_kernel_for<1, U, 4>(layout);
-        default: return batch_kernel_for<1, U, kMaxPrefetchChunks>(layout);
+        case 2: return prefetch_kernel_split<U, 2>(layout, split);
+        case 4: return prefetch_kernel_split<U, 4>(layout, split);
+        default: return prefetch_kernel_split<U, kMaxPrefetchChunks>(layout, split);
     }
 }
 
 // The kernel of a batch: rows per task group, weight layout, activation
-// chunks prefetched per thread (0: none) and units per thread.
-BatchKernel batch_kernel(int mr, int layout, int prefetch, int upt) {
+// chunks prefetched per thread (0: none), units per thread and waves per
+// unit.
+BatchKernel batch_kernel(int mr, int layout, int prefetch, int upt, int split) {
     if (mr != 1) return batch_kernel_for<4, units_per_thread(4), 0>(layout);
     if (prefetch == 0) return batch_kernel_for<1, units_per_thread(1), 0>(layout);
-    return upt == 1 ? prefetch_kernel<1>(layout, prefetch) : prefetch_kernel<units_per_thread(1)>(layout, prefetch);
+    return upt == 1 ? prefetch_kernel<1>(layout, prefetch, split)
+                    : prefetch_kernel<units_per_thread(1)>(layout, prefetch, split);
 }
 
 }  // namespace
@@ -1471,6 +1626,17 @@ int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_
     batch->upt = upt;
     if (prefetch_candidate)
         for (const Q4Task &t : host) batch->prefetch = std::max(batch->prefetch, prefetch_chunks(t));
+    if (prefetch_candidate && upt == 1 && kSplitUnits) {
+        // Items of at most 64 (128) units: each unit split over 4 (2) waves.
+        // Measured on MI355X, the staged decode of cfg3 (q/k/v items of 88
+        // units, o of 64): 0.397 -> 0.384 ms per step.  Narrowing the gate/up
+        // and down tiles (176 units) so that they split too was slower (0.404
+        // ms for two waves per unit, 0.427 for four): each extra workgroup
+        // quantises the whole activation row again.
+        int max_units = 0;
+        for (const Q4Task &t : host) max_units = std::max(max_units, t.cpw * (t.blocks / 8));
+        batch->split = max_units <= kLaneGroup ? 4 : max_units <= 2 * kLaneGroup ? 2 : 1;
+    }
     batch->lds = lds;
     if (kArgBatches && count <= static_cast<uint32_t>(kArgTasks)) {
         batch->in_args = true;
@@ -1495,7 +1661,7 @@ int qxt_q4_0_batch_launch(const qxt_q4_0_batch *batch, void *stream) {
                     as_stream(stream), batch->jobs, batch->chunks);
         if (rc != QXT_OK) return rc;
     }
-    const BatchKernel kernel = batch_kernel(batch->mr, batch->layout, batch->prefetch, batch->upt);
+    const BatchKernel kernel = batch_kernel(batch->mr, batch->layout, batch->prefetch, batch->upt, batch->split);
     if (batch->in_args)
         return launch("q4_0_batch_kernel", kernel.args, dim3(batch->grid), dim3(kThreads), batch->lds,
                       as_stream(stream), batch->args);

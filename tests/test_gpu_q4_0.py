@@ -271,6 +271,25 @@ def test_batch_in_kernel_arguments_and_in_device_tables_bit_exact(count: int) ->
         del graph
 
 
+@pytest.mark.parametrize("shapes", [
+    [(1, 2048, 2048, 0, 2048), (1, 2048, 256, 0, 256), (1, 2048, 256, 0, 256)],  # q/k/v-like items
+    [(1, 2048, 300, 4, 290), (1, 256, 40, 0, 40)],                                  # narrow items
+    [(1, 5632, 2048, 0, 2048)],                                                       # down-like items
+])
+def test_stage_batch_mixing_lane_and_native_weights_bit_exact(shapes) -> None:
+    # One prefetching stage batch whose tasks alternate lane-layout and native
+    # weights (the kernel then chooses the load form per task), for item widths
+    # whose units are split over four, two or one waves.
+    tasks, expected = _batch_case(90 + len(shapes), shapes, fused_every=1)
+    for i, t in enumerate(tasks):
+        if i % 2 == 0:
+            t["weight"] = q4.pack_ggml_q4_0_lane_weights(t["weight"])
+    with q4.Q4_0LinearBatch(tasks) as batch:
+        batch.launch()
+        torch.cuda.synchronize()
+    _check_batch(tasks, expected)
+
+
 @pytest.mark.parametrize("k", [2048, 5632])
 def test_stage_batch_activation_blocks_outside_the_fast_scale_range_bit_exact(k: int) -> None:
     # The prefetching stage kernels quantise their fp32 row with the
