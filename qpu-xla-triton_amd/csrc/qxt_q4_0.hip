@@ -227,18 +227,18 @@ __host__ __device__ inline int prefetch_chunks(const Q4Task &t) {
     return chunks <= 2 ? 2 : chunks <= 4 ? 4 : chunks <= kMaxPrefetchChunks ? kMaxPrefetchChunks : 0;
 }
 
-template <int PC>
+template <int PC, int NT = kThreads>
 __device__ __forceinline__ void prefetch_row(const Q4Task &t, float4 (&xv)[PC]) {
     const int total = t.blocks * 8;
 #pragma unroll
     for (int u = 0; u < PC; ++u) {
         // Unconditional loads (lanes past the row re-read its last chunk, unused).
-        const int e = min(u * kThreads + static_cast<int>(threadIdx.x), total - 1);
+        const int e = min(u * NT + static_cast<int>(threadIdx.x), total - 1);
         xv[u] = load_float4(reinterpret_cast<const uint8_t *>(t.x) + e * 16);
     }
 }
 
-template <int PC>
+template <int PC, int NT = kThreads>
 __device__ __forceinline__ void quantise_row(const Q4Task &t, const float4 (&xv)[PC], int *aq, int *ad,
                                              const Q4Lds &geo) {
     const int total = t.blocks * 8;  // a multiple of 8: whole 8-lane groups
@@ -252,13 +252,13 @@ __device__ __forceinline__ void quantise_row(const Q4Task &t, const float4 (&xv)
     bool exact = true;
 #pragma unroll
     for (int u = 0; u < PC; ++u) {
-        const int e = u * kThreads + threadIdx.x;
+        const int e = u * NT + threadIdx.x;
         exact &= quantise_chunk<false, true>(xv[u], 0, min(e, total - 1), aq, ad, geo, e < total);
     }
     if (!exact) {
 #pragma unroll
         for (int u = 0; u < PC; ++u) {
-            const int e = u * kThreads + threadIdx.x;
+            const int e = u * NT + threadIdx.x;
             quantise_chunk(xv[u], 0, min(e, total - 1), aq, ad, geo, e < total);
         }
     }
@@ -811,11 +811,11 @@ __global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Task t) {
 // compile-time choice: under a run-time branch the compiler cannot count
 // the weight loads issued after it and waits for all of them.
 //
-// S > 1 (one-row prefetch batches of at most 64 * 4 / S units per item):
-// each unit is split over S waves.  Wave w takes part w % S -- blocks
-// [8/S * part, +8/S) -- of units 64 * (w / S) + lane, loading only the
-// 16-byte chunks that hold them, so each wave's share of the block dots is
-// 1/S of a unit instead of a whole unit on fewer lanes.
+// S > 1 (one-row prefetch batches of at most 64 * (NT / 64) / S units per
+// item, NT = 256 or 512 threads): each unit is split over S waves.  Wave w
+// takes part w % S -- blocks [8/S * part, +8/S) -- of units 64 * (w / S) +
+// lane, loading only the 16-byte chunks that hold them, so each wave's share
+// of the block dots is 1/S of a unit instead of a whole unit on fewer lanes.
 
 // Part P (of S) of a unit: blocks [8/S * P, +8/S), which lie in 16-byte
 // chunks [2P, 2P + 2] (S = 4) or [4P, 4P + 4] (S = 2) -- block i of a
@@ -907,7 +907,7 @@ __device__ __forceinline__ void compute_part(int G, int units, int u, const uint
     else *reinterpret_cast<float2 *>(dst) = make_float2(terms[0], terms[1]);
 }
 
-template <int LAYOUT, int PC, int S>
+template <int LAYOUT, int PC, int S, int NT = kThreads>
 __device__ __forceinline__ void batch_item_split(const Q4Task &t, int col_base, int ncols) {
     static_assert(S == 2 || S == 4, "a unit splits into 2 or 4 parts");
     extern __shared__ int lds[];
@@ -915,7 +915,7 @@ __device__ __forceinline__ void batch_item_split(const Q4Task &t, int col_base, 
     const int G = B >> 3;
     const int units = ncols * G;
     float4 xv[PC];
-    prefetch_row<PC>(t, xv);
+    prefetch_row<PC, NT>(t, xv);
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int part = wave % S;
     const int u = (wave / S) * 64 + static_cast<int>(threadIdx.x & 63);
@@ -925,7 +925,7 @@ __device__ __forceinline__ void batch_item_split(const Q4Task &t, int col_base, 
     int *aq = lds;
     int *ad = aq + geo.aq_row;
     float *cb = reinterpret_cast<float *>(ad + geo.ad_row);
-    quantise_row<PC>(t, xv, aq, ad, geo);
+    quantise_row<PC, NT>(t, xv, aq, ad, geo);
     __syncthreads();
     if constexpr (S == 2) {
         if (part == 0) compute_part<2, 0>(G, units, u, pr, aq, ad, cb, geo);
@@ -939,7 +939,7 @@ __device__ __forceinline__ void batch_item_split(const Q4Task &t, int col_base, 
         }
     }
     __syncthreads();
-    sum_store<1, true>(t, col_base, 0, ncols, cb, geo);
+    sum_store<1, true, NT>(t, col_base, 0, ncols, cb, geo);
 }
 
 template <int MR, int U, int LAYOUT, int PC>
@@ -965,17 +965,17 @@ __device__ __forceinline__ void batch_item(const Q4Task &t, int col_base, int nc
     sum_store<MR, true>(t, col_base, 0, ncols, cb, geo);
 }
 
-template <int MR, int U, int LAYOUT, int PC, int S = 1>
+template <int MR, int U, int LAYOUT, int PC, int S = 1, int NT = kThreads>
 __device__ __forceinline__ void batch_item_any(const Q4Task &t, int col_base, int ncols) {
-    if constexpr (S > 1) batch_item_split<LAYOUT, PC, S>(t, col_base, ncols);
+    if constexpr (S > 1) batch_item_split<LAYOUT, PC, S, NT>(t, col_base, ncols);
     else batch_item<MR, U, LAYOUT, PC>(t, col_base, ncols);
 }
 
-template <int MR, int U, int LAYOUT, int PC, int S = 1>
-__global__ __launch_bounds__(kThreads) void q4_0_batch_kernel(const Q4Task *__restrict__ tasks,
-                                                              const Q4Item *__restrict__ items) {
+template <int MR, int U, int LAYOUT, int PC, int S = 1, int NT = kThreads>
+__global__ __launch_bounds__(NT) void q4_0_batch_kernel(const Q4Task *__restrict__ tasks,
+                                                        const Q4Item *__restrict__ items) {
     const Q4Item item = items[blockIdx.x];
-    batch_item_any<MR, U, LAYOUT, PC, S>(tasks[item.task], item.col_base, item.ncols);
+    batch_item_any<MR, U, LAYOUT, PC, S, NT>(tasks[item.task], item.col_base, item.ncols);
 }
 
 // A batch of at most kArgTasks tasks travels in the kernel arguments: each
@@ -990,15 +990,15 @@ struct Q4ArgBatch {
     Q4Task task[kArgTasks];
 };
 
-template <int MR, int U, int LAYOUT, int PC, int S = 1>
-__global__ __launch_bounds__(kThreads) void q4_0_arg_batch_kernel(Q4ArgBatch a) {
+template <int MR, int U, int LAYOUT, int PC, int S = 1, int NT = kThreads>
+__global__ __launch_bounds__(NT) void q4_0_arg_batch_kernel(Q4ArgBatch a) {
     const int i = static_cast<int>(blockIdx.x);
     int ti = 0;
 #pragma unroll
     for (int j = 1; j < kArgTasks; ++j) ti += i >= a.first_item[j] ? 1 : 0;
     const Q4Task t = a.task[ti];
     const int col_base = (i - a.first_item[ti]) * t.cpw;
-    batch_item_any<MR, U, LAYOUT, PC, S>(t, col_base, min(t.cpw, t.ncols - col_base));
+    batch_item_any<MR, U, LAYOUT, PC, S, NT>(t, col_base, min(t.cpw, t.ncols - col_base));
 }
 
 // The four-row matrix-core tiles (compute_mfma4): workgroup (x, y) of NT
@@ -1086,6 +1086,10 @@ constexpr bool kPrefetchLargeBatches = QXT_PREFETCH_LARGE != 0;
 #define QXT_SPLIT_UNITS 1
 #endif
 constexpr bool kSplitUnits = QXT_SPLIT_UNITS != 0;
+#ifndef QXT_WIDE_SPLIT
+#define QXT_WIDE_SPLIT 1
+#endif
+constexpr bool kWideSplit = QXT_WIDE_SPLIT != 0;
 
 #ifndef QXT_ARG_BATCH
 #define QXT_ARG_BATCH 1
@@ -1232,6 +1236,7 @@ struct qxt_q4_0_batch {
     int prefetch = 0;  // activation chunks per thread prefetched (every task one fp32 row), or 0
     int upt = 1;       // units per thread of the batch kernel
     int split = 1;     // waves per unit (one-row prefetch batches of narrow items)
+    bool wide = false; // 512-thread workgroups (split 2 or 4)
     size_t lds = 0;
     bool in_args = false;  // tasks and items travel in the kernel arguments
     Q4ArgBatch args{};
@@ -1247,21 +1252,25 @@ struct BatchKernel {
     void (*args)(Q4ArgBatch);
 };
 
-template <int MR, int U, int LAYOUT, int PC, int S>
+template <int MR, int U, int LAYOUT, int PC, int S, int NT>
 BatchKernel batch_kernels() {
-    return {q4_0_batch_kernel<MR, U, LAYOUT, PC, S>, q4_0_arg_batch_kernel<MR, U, LAYOUT, PC, S>};
+    return {q4_0_batch_kernel<MR, U, LAYOUT, PC, S, NT>, q4_0_arg_batch_kernel<MR, U, LAYOUT, PC, S, NT>};
 }
 
-template <int MR, int U, int PC, int S = 1>
+template <int MR, int U, int PC, int S = 1, int NT = kThreads>
 BatchKernel batch_kernel_for(int layout) {
-    return layout == kLaneLayout    ? batch_kernels<MR, U, kLaneLayout, PC, S>()
-           : layout == kNativeRows ? batch_kernels<MR, U, kNativeRows, PC, S>()
-                                   : batch_kernels<MR, U, kEitherLayout, PC, S>();
+    return layout == kLaneLayout    ? batch_kernels<MR, U, kLaneLayout, PC, S, NT>()
+           : layout == kNativeRows ? batch_kernels<MR, U, kNativeRows, PC, S, NT>()
+                                   : batch_kernels<MR, U, kEitherLayout, PC, S, NT>();
 }
 
+// One-row prefetch batches.  split: waves per unit; wide: 512-thread
+// workgroups (the row's chunks over twice the threads).
 template <int U, int PC>
-BatchKernel prefetch_kernel_split(int layout, int split) {
+BatchKernel prefetch_kernel_split(int layout, int split, bool wide) {
     if constexpr (U == 1) {
+        if (wide && split == 4) return batch_kernel_for<1, 1, (PC + 1) / 2, 4, 2 * kThreads>(layout);
+        if (wide) return batch_kernel_for<1, 1, (PC + 1) / 2, 2, 2 * kThreads>(layout);
         if (split == 4) return batch_kernel_for<1, 1, PC, 4>(layout);
         if (split == 2) return batch_kernel_for<1, 1, PC, 2>(layout);
     }
@@ -1269,22 +1278,22 @@ BatchKernel prefetch_kernel_split(int layout, int split) {
 }
 
 template <int U>
-BatchKernel prefetch_kernel(int layout, int prefetch, int split) {
+BatchKernel prefetch_kernel(int layout, int prefetch, int split, bool wide) {
     switch (prefetch) {
-        case 2: return prefetch_kernel_split<U, 2>(layout, split);
-        case 4: return prefetch_kernel_split<U, 4>(layout, split);
-        default: return prefetch_kernel_split<U, kMaxPrefetchChunks>(layout, split);
+        case 2: return prefetch_kernel_split<U, 2>(layout, split, wide);
+        case 4: return prefetch_kernel_split<U, 4>(layout, split, wide);
+        default: return prefetch_kernel_split<U, kMaxPrefetchChunks>(layout, split, wide);
     }
 }
 
 // The kernel of a batch: rows per task group, weight layout, activation
 // chunks prefetched per thread (0: none), units per thread and waves per
 // unit.
-BatchKernel batch_kernel(int mr, int layout, int prefetch, int upt, int split) {
+BatchKernel batch_kernel(int mr, int layout, int prefetch, int upt, int split, bool wide) {
     if (mr != 1) return batch_kernel_for<4, units_per_thread(4), 0>(layout);
     if (prefetch == 0) return batch_kernel_for<1, units_per_thread(1), 0>(layout);
-    return upt == 1 ? prefetch_kernel<1>(layout, prefetch, split)
-                    : prefetch_kernel<units_per_thread(1)>(layout, prefetch, split);
+    return upt == 1 ? prefetch_kernel<1>(layout, prefetch, split, wide)
+                    : prefetch_kernel<units_per_thread(1)>(layout, prefetch, split, wide);
 }
 
 }  // namespace
@@ -1636,6 +1645,14 @@ int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_
         int max_units = 0;
         for (const Q4Task &t : host) max_units = std::max(max_units, t.cpw * (t.blocks / 8));
         batch->split = max_units <= kLaneGroup ? 4 : max_units <= 2 * kLaneGroup ? 2 : 1;
+        // Items of more than 64 units: 512-thread workgroups, so that a unit
+        // still splits over two (129-256 units) or four (65-128) of their
+        // eight waves and each thread quantises half as many row chunks
+        // (measured on MI355X, the staged decode of cfg3, gate/up and down
+        // items of 176 units: 0.384 -> 0.374 ms; q/k/v items of 88 units over
+        // four of eight waves instead of two of four: 0.364 -> 0.361 ms).
+        batch->wide = kWideSplit && batch->split < 4;
+        if (batch->wide) batch->split = std::min(4, 2 * batch->split);
     }
     batch->lds = lds;
     if (kArgBatches && count <= static_cast<uint32_t>(kArgTasks)) {
@@ -1661,12 +1678,14 @@ int qxt_q4_0_batch_launch(const qxt_q4_0_batch *batch, void *stream) {
                     as_stream(stream), batch->jobs, batch->chunks);
         if (rc != QXT_OK) return rc;
     }
-    const BatchKernel kernel = batch_kernel(batch->mr, batch->layout, batch->prefetch, batch->upt, batch->split);
+    const BatchKernel kernel =
+        batch_kernel(batch->mr, batch->layout, batch->prefetch, batch->upt, batch->split, batch->wide);
+    const dim3 block(batch->wide ? 2 * kThreads : kThreads);
     if (batch->in_args)
-        return launch("q4_0_batch_kernel", kernel.args, dim3(batch->grid), dim3(kThreads), batch->lds,
-                      as_stream(stream), batch->args);
-    return launch("q4_0_batch_kernel", kernel.tables, dim3(batch->grid), dim3(kThreads), batch->lds,
-                  as_stream(stream), batch->tasks, batch->items);
+        return launch("q4_0_batch_kernel", kernel.args, dim3(batch->grid), block, batch->lds, as_stream(stream),
+                      batch->args);
+    return launch("q4_0_batch_kernel", kernel.tables, dim3(batch->grid), block, batch->lds, as_stream(stream),
+                  batch->tasks, batch->items);
 }
 
 uint32_t qxt_q4_0_batch_work_items(const qxt_q4_0_batch *batch) { return batch == nullptr ? 0 : batch->item_count; }
