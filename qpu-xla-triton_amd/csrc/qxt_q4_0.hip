@@ -376,6 +376,42 @@ __device__ __forceinline__ void stage_q8_rows(const Q4Task &t, const Q8RowRegs<N
     }
 }
 
+// One native Q8_0 activation row (blocks <= 512) into registers, 512 / NT
+// blocks per thread, with unconditional loads (indexes clamped into the row)
+// like fetch_q8_rows; stage_q8_row writes its LDS image with the row-major
+// records.
+template <int NT>
+__device__ __forceinline__ void fetch_q8_row(const Q4Task &t, Q8RowRegs<NT> &a) {
+#pragma unroll
+    for (int i = 0; i < Q8RowRegs<NT>::kItems; ++i) {
+        const int b = min(static_cast<int>(threadIdx.x) + i * NT, t.blocks - 1);
+        const QXT_GLOBAL uint16_t *p = global_in<uint16_t>(t.act + static_cast<size_t>(b) * Q8_0_BYTES);
+#pragma unroll
+        for (int k = 0; k < 17; ++k) a.h[i][k] = p[k];
+    }
+}
+
+template <int NT>
+__device__ __forceinline__ void stage_q8_row(const Q4Task &t, const Q8RowRegs<NT> &a, int *aq, int *ad,
+                                             const Q4Lds &geo) {
+#pragma unroll
+    for (int i = 0; i < Q8RowRegs<NT>::kItems; ++i) {
+        const int b = static_cast<int>(threadIdx.x) + i * NT;
+        if (b >= t.blocks) break;
+        int words[8];
+        int sum = 0;
+#pragma unroll
+        for (int h = 0; h < 8; ++h) {
+            words[h] = static_cast<int>(a.h[i][1 + 2 * h] | (a.h[i][2 + 2 * h] << 16));
+            sum = dot4(words[h], 0x01010101, sum);  // sum of the four signed bytes
+        }
+        int *dstq = aq + aq_index(b, 0);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dstq[j] = words[j];
+        store_scale_sum<false>(ad, geo, 0, b, half_bits_to_float(a.h[i][0]), sum);
+    }
+}
+
 // Weight layout of a kernel instantiation: native rows, lane layout, or
 // either (read from the task).  Separate instantiations keep the lane
 // layout's non-temporal loads from being merged with the native rows'
@@ -914,8 +950,12 @@ __device__ __forceinline__ void batch_item_split(const Q4Task &t, int col_base, 
     const int B = t.blocks;
     const int G = B >> 3;
     const int units = ncols * G;
-    float4 xv[PC];
-    prefetch_row<PC, NT>(t, xv);
+    // The activation is requested before the weights: an fp32 row (PC > 0,
+    // quantised here) or a native Q8_0 row (PC == 0, blocks <= 512).
+    float4 xv[PC > 0 ? PC : 1];
+    Q8RowRegs<NT> a8;
+    if constexpr (PC > 0) prefetch_row<PC, NT>(t, xv);
+    else fetch_q8_row<NT>(t, a8);
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int part = wave % S;
     const int u = (wave / S) * 64 + static_cast<int>(threadIdx.x & 63);
@@ -925,7 +965,8 @@ __device__ __forceinline__ void batch_item_split(const Q4Task &t, int col_base, 
     int *aq = lds;
     int *ad = aq + geo.aq_row;
     float *cb = reinterpret_cast<float *>(ad + geo.ad_row);
-    quantise_row<PC, NT>(t, xv, aq, ad, geo);
+    if constexpr (PC > 0) quantise_row<PC, NT>(t, xv, aq, ad, geo);
+    else stage_q8_row<NT>(t, a8, aq, ad, geo);
     __syncthreads();
     if constexpr (S == 2) {
         if (part == 0) compute_part<2, 0>(G, units, u, pr, aq, ad, cb, geo);
@@ -1049,6 +1090,15 @@ __global__ __launch_bounds__(NT) void q4_0_mfma4_kernel(Q4Task t) {
     sum_store<MR, true, NT>(t, col_base, r0, tile_cols, cb, geo);
 }
 
+// A one-row single linear over native Q8_0 activations whose tiles hold at
+// most 256 units: the stage kernels' split units (batch_item_split), one
+// workgroup per column tile.
+template <int LAYOUT, int S, int NT>
+__global__ __launch_bounds__(NT) void q4_0_split_kernel(Q4Task t) {
+    const int col_base = static_cast<int>(blockIdx.x) * t.cpw;
+    batch_item_split<LAYOUT, 0, S, NT>(t, col_base, min(t.cpw, t.ncols - col_base));
+}
+
 // Threads per matrix-core tile workgroup (measured on MI355X, cfg2 back to
 // back: 512 threads, two waves per SIMD, 11.2 / 6.8 us against 9.7 / 5.5 us
 // with 256 at N = 11008 / 4096).
@@ -1090,6 +1140,11 @@ constexpr bool kSplitUnits = QXT_SPLIT_UNITS != 0;
 #define QXT_WIDE_SPLIT 1
 #endif
 constexpr bool kWideSplit = QXT_WIDE_SPLIT != 0;
+
+#ifndef QXT_SPLIT_SINGLE
+#define QXT_SPLIT_SINGLE 1
+#endif
+constexpr bool kSplitSingle = QXT_SPLIT_SINGLE != 0;
 
 #ifndef QXT_ARG_BATCH
 #define QXT_ARG_BATCH 1
@@ -1167,6 +1222,27 @@ int launch_single(Q4Task t, hipStream_t stream) {
                                         dim3(kMfma4Threads), lds, stream, t)
                                : launch(name, q4_0_mfma4_kernel<kNativeRows, kMfma4Threads>, grid,
                                         dim3(kMfma4Threads), lds, stream, t);
+        if constexpr (MR == 1) {
+            const int units = t.cpw * G;
+            if (kSplitSingle && fast && t.x == nullptr && t.blocks <= 512 && units <= 4 * kLaneGroup) {
+                // Tiles of at most 64 units: 4 waves of 256 threads per unit;
+                // more: 512 threads, 4 (up to 128 units) or 2 waves per unit.
+                if (units <= kLaneGroup)
+                    return t.lanes ? launch(name, q4_0_split_kernel<kLaneLayout, 4, kThreads>, grid, dim3(kThreads),
+                                            lds, stream, t)
+                                   : launch(name, q4_0_split_kernel<kNativeRows, 4, kThreads>, grid, dim3(kThreads),
+                                            lds, stream, t);
+                if (units <= 2 * kLaneGroup)
+                    return t.lanes ? launch(name, q4_0_split_kernel<kLaneLayout, 4, 2 * kThreads>, grid,
+                                            dim3(2 * kThreads), lds, stream, t)
+                                   : launch(name, q4_0_split_kernel<kNativeRows, 4, 2 * kThreads>, grid,
+                                            dim3(2 * kThreads), lds, stream, t);
+                return t.lanes ? launch(name, q4_0_split_kernel<kLaneLayout, 2, 2 * kThreads>, grid,
+                                        dim3(2 * kThreads), lds, stream, t)
+                               : launch(name, q4_0_split_kernel<kNativeRows, 2, 2 * kThreads>, grid,
+                                        dim3(2 * kThreads), lds, stream, t);
+            }
+        }
         if (fast && t.lanes)
             return launch(name, q4_0_linear_kernel<MR, U, true, false, kLaneLayout>, grid, dim3(kThreads), lds, stream,
                           t);
