@@ -1090,6 +1090,140 @@ __global__ __launch_bounds__(NT) void q4_0_mfma4_kernel(Q4Task t) {
     sum_store<MR, true, NT>(t, col_base, r0, tile_cols, cb, geo);
 }
 
+// The four-row matrix-core tiles with each unit split over two waves of a
+// 512-thread workgroup: wave w computes blocks [4 (w & 1), +4) of the units
+// of wave w >> 1 of q4_0_mfma4_kernel<LAYOUT, 256>, loading only the five
+// 16-byte chunks [4 (w & 1), +5) that hold them (one code path for both
+// halves, the chunk offset being the same for the whole wave).
+__device__ __forceinline__ int mfma4_split_unit(int lg, int first) {
+    const int lane = threadIdx.x & 63;
+    const int b = lane >> 2, p = lane & 3;
+    const int perm = ((((b >> lg) << 2) + p) << lg) + (b & ((1 << lg) - 1));
+    return first + ((static_cast<int>(threadIdx.x) >> 7) << 6) + perm;
+}
+
+template <int LAYOUT>
+__device__ __forceinline__ void load_mfma4_half(const Q4Task &t, int col_base, int lg, int units, int first, int c0,
+                                                uint32_t (&d)[20]) {
+    const int u = min(mfma4_split_unit(lg, first), units - 1);
+    const int col = u >> lg, g = u & ((1 << lg) - 1);
+    const QXT_GLOBAL v4u *src;
+    if constexpr (LAYOUT == kLaneLayout) {
+        const size_t unit = (static_cast<size_t>(t.wcol0 + col_base + col) << lg) + g;
+        src = global_in<v4u>(t.w + (unit / kLaneGroup) * kGroupBytes + (unit % kLaneGroup) * 16) + c0 * kLaneGroup;
+    } else {
+        src = global_in<v4u>(t.w + static_cast<size_t>(t.wcol0 + col_base + col) * t.w_stride +
+                             static_cast<size_t>(g) * 144) +
+              c0;
+    }
+#pragma unroll
+    for (int v = 0; v < 5; ++v) {
+        const v4u x = LAYOUT == kLaneLayout ? __builtin_nontemporal_load(src + v * kLaneGroup) : src[v];
+        d[4 * v + 0] = x[0];
+        d[4 * v + 1] = x[1];
+        d[4 * v + 2] = x[2];
+        d[4 * v + 3] = x[3];
+    }
+}
+
+template <int H>
+__device__ __forceinline__ void compute_mfma4_half(int lg, int units, int first, const uint32_t (&pr)[20],
+                                                   const int *aq, const int *ad, float *cb, const Q4Lds &geo,
+                                                   int cpw) {
+    typedef int v4i_t __attribute__((ext_vector_type(4)));
+    const int lane = threadIdx.x & 63;
+    const int b = lane >> 2, p = lane & 3;
+    const int g = b & ((1 << lg) - 1);
+    const int *arow = aq + p * geo.aq_row;
+    const int u = mfma4_split_unit(lg, first);
+    const int col = u >> lg;
+    uint32_t d[36];  // the unit's words at their places (register renaming only)
+#pragma unroll
+    for (int k = 0; k < 20; ++k) d[16 * H + k] = pr[k];
+    float terms[4][4];
+    auto do_block = [&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        constexpr int I = 4 * H + i;
+        uint32_t sbits, qs[4];
+        unit_block<I>(d, sbits, qs);
+        const int bg = g * 8 + I;
+        const int4 lo = *reinterpret_cast<const int4 *>(arow + aq_index(bg, 0));
+        const int4 hi = *reinterpret_cast<const int4 *>(arow + aq_index(bg, 4));
+        const int4 s8 = *reinterpret_cast<const int4 *>(ad + aq_index(bg, 0));
+        const float4 da = *reinterpret_cast<const float4 *>(ad + aq_index(bg, 4));
+        v4i_t acc = {s8.x, s8.y, s8.z, s8.w};
+        acc = __builtin_amdgcn_mfma_i32_4x4x4i8(lo.x, static_cast<int>(qs[0] & 0x0F0F0F0Fu), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_4x4x4i8(lo.y, static_cast<int>(qs[1] & 0x0F0F0F0Fu), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_4x4x4i8(lo.z, static_cast<int>(qs[2] & 0x0F0F0F0Fu), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_4x4x4i8(lo.w, static_cast<int>(qs[3] & 0x0F0F0F0Fu), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_4x4x4i8(hi.x, static_cast<int>((qs[0] >> 4) & 0x0F0F0F0Fu), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_4x4x4i8(hi.y, static_cast<int>((qs[1] >> 4) & 0x0F0F0F0Fu), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_4x4x4i8(hi.z, static_cast<int>((qs[2] >> 4) & 0x0F0F0F0Fu), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_4x4x4i8(hi.w, static_cast<int>((qs[3] >> 4) & 0x0F0F0F0Fu), acc, 0, 0, 0);
+        const float dw = half_bits_to_float(sbits);
+        const float das[4] = {da.x, da.y, da.z, da.w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float v = static_cast<float>(acc[r]) * dw;
+            v = v * das[r];
+            terms[r][i] = v;
+        }
+    };
+    do_block(std::integral_constant<int, 0>{});
+    do_block(std::integral_constant<int, 1>{});
+    do_block(std::integral_constant<int, 2>{});
+    do_block(std::integral_constant<int, 3>{});
+    if (u < units) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            *reinterpret_cast<float4 *>(cb + (r * cpw + col) * geo.cbs + g * 8 + 4 * H) =
+                make_float4(terms[r][0], terms[r][1], terms[r][2], terms[r][3]);
+    }
+}
+
+template <int LAYOUT>
+__global__ __launch_bounds__(2 * kThreads) void q4_0_mfma4_split_kernel(Q4Task t) {
+    constexpr int MR = 4, NT = 2 * kThreads;
+    extern __shared__ int lds[];
+    const int col_base = blockIdx.x * t.cpw;
+    const int r0 = blockIdx.y * MR;
+    const int B = t.blocks;
+    const Q4Lds geo(B, true);
+    int *aq = lds;
+    int *ad = aq + MR * geo.aq_row;
+    float *cb = reinterpret_cast<float *>(ad + MR * geo.ad_row);
+    const int tile_cols = min(t.cpw, t.ncols - col_base);
+    const int G = B >> 3;
+    const int units = tile_cols * G;
+    const int half = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)) & 1;
+    const int c0 = 4 * half;
+    Q8RowRegs<NT> a;
+    fetch_q8_rows(t, r0, a);
+    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads first
+    const int lg = __builtin_ctz(G);
+    constexpr int R = NT / 2;  // units per round: two waves per unit
+    uint32_t wr[20], wn[20];
+    load_mfma4_half<LAYOUT>(t, col_base, lg, units, 0, c0, wr);
+    load_mfma4_half<LAYOUT>(t, col_base, lg, units, R, c0, wn);
+    __builtin_amdgcn_sched_barrier(0);
+    stage_q8_rows(t, a, aq, ad, geo);
+    __syncthreads();
+    auto compute = [&](int first, const uint32_t (&pr)[20]) {
+        if (half == 0) compute_mfma4_half<0>(lg, units, first, pr, aq, ad, cb, geo, t.cpw);
+        else compute_mfma4_half<1>(lg, units, first, pr, aq, ad, cb, geo, t.cpw);
+    };
+    for (int first = 0;;) {
+        compute(first, wr);
+        load_mfma4_half<LAYOUT>(t, col_base, lg, units, first + 2 * R, c0, wr);
+        if ((first += R) >= units) break;
+        compute(first, wn);
+        load_mfma4_half<LAYOUT>(t, col_base, lg, units, first + 2 * R, c0, wn);
+        if ((first += R) >= units) break;
+    }
+    __syncthreads();
+    sum_store<MR, true, NT>(t, col_base, r0, tile_cols, cb, geo);
+}
+
 // A one-row single linear over native Q8_0 activations whose tiles hold at
 // most 256 units: the stage kernels' split units (batch_item_split), one
 // workgroup per column tile.
@@ -1140,6 +1274,11 @@ constexpr bool kSplitUnits = QXT_SPLIT_UNITS != 0;
 #define QXT_WIDE_SPLIT 1
 #endif
 constexpr bool kWideSplit = QXT_WIDE_SPLIT != 0;
+
+#ifndef QXT_MFMA4_SPLIT
+#define QXT_MFMA4_SPLIT 1
+#endif
+constexpr bool kMfma4Split = QXT_MFMA4_SPLIT != 0;
 
 #ifndef QXT_SPLIT_SINGLE
 #define QXT_SPLIT_SINGLE 1
@@ -1218,10 +1357,21 @@ int launch_single(Q4Task t, hipStream_t stream) {
         const int G = t.blocks / 8;
         if constexpr (MR == 4)
             if (fast && t.x == nullptr && G <= 16 && 16 % G == 0)
+            {
+                // Tiles of several rounds: each unit over two waves of 512
+                // (measured on MI355X, cfg2 back to back: N = 11008, three
+                // rounds, 9.7 -> 9.3 us; N = 4096, one round, 5.5 -> 5.65 us,
+                // so single-round tiles keep one wave per unit).
+                if (kMfma4Split && t.cpw * G > kMfma4Threads)
+                    return t.lanes ? launch(name, q4_0_mfma4_split_kernel<kLaneLayout>, grid, dim3(2 * kThreads), lds,
+                                            stream, t)
+                                   : launch(name, q4_0_mfma4_split_kernel<kNativeRows>, grid, dim3(2 * kThreads),
+                                            lds, stream, t);
                 return t.lanes ? launch(name, q4_0_mfma4_kernel<kLaneLayout, kMfma4Threads>, grid,
                                         dim3(kMfma4Threads), lds, stream, t)
                                : launch(name, q4_0_mfma4_kernel<kNativeRows, kMfma4Threads>, grid,
                                         dim3(kMfma4Threads), lds, stream, t);
+            }
         if constexpr (MR == 1) {
             const int units = t.cpw * G;
             if (kSplitSingle && fast && t.x == nullptr && t.blocks <= 512 && units <= 4 * kLaneGroup) {

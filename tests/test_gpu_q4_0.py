@@ -75,6 +75,7 @@ def test_reference_seed_fixture_bit_exact_and_block_dots() -> None:
         (8, 128, 4100),   # two row groups of wide tiles, three rounds per workgroup
         (6, 16, 130),     # four-row matrix-core tiles over native rows, two block ranges per unit
         (4, 32, 77),      # four block ranges per unit
+        (4, 64, 9000),    # eight block ranges per unit, tiles of several rounds
     ],
 )
 def test_random_shapes_bit_exact(rows: int, blocks: int, outputs: int) -> None:
@@ -443,6 +444,7 @@ def test_lane_pack_kernel_matches_the_layout_definition(n: int, blocks: int) -> 
     (6, 512, 130, 2, 128),      # two, a partial second row group
     (5, 1024, 200, 3, 190),     # four, one row in the second row group
     (4, 2048, 300, 0, 300),     # eight
+    (4, 2048, 9000, 3, 8990),   # eight, tiles of several rounds (units over two waves each)
 ])
 def test_lane_linear_bit_exact_against_oracle(rows: int, k: int, n: int, wcol0: int, ncols: int) -> None:
     rng = np.random.default_rng(5000 + rows + n)
