@@ -329,7 +329,7 @@ __device__ __forceinline__ void stage_activation(const Q4Task &t, int r0, int *a
 // exactly and the staging waits only for these.
 template <int NT>
 struct Q8RowRegs {
-    static constexpr int kItems = 512 / NT;
+    static constexpr int kItems = (512 + NT - 1) / NT;
     uint32_t h[kItems][17];
 };
 
@@ -1095,17 +1095,18 @@ __global__ __launch_bounds__(NT) void q4_0_mfma4_kernel(Q4Task t) {
 // of wave w >> 1 of q4_0_mfma4_kernel<LAYOUT, 256>, loading only the five
 // 16-byte chunks [4 (w & 1), +5) that hold them (one code path for both
 // halves, the chunk offset being the same for the whole wave).
+template <int S>
 __device__ __forceinline__ int mfma4_split_unit(int lg, int first) {
     const int lane = threadIdx.x & 63;
     const int b = lane >> 2, p = lane & 3;
     const int perm = ((((b >> lg) << 2) + p) << lg) + (b & ((1 << lg) - 1));
-    return first + ((static_cast<int>(threadIdx.x) >> 7) << 6) + perm;
+    return first + (((static_cast<int>(threadIdx.x) >> 6) / S) << 6) + perm;
 }
 
-template <int LAYOUT>
+template <int LAYOUT, int S>
 __device__ __forceinline__ void load_mfma4_half(const Q4Task &t, int col_base, int lg, int units, int first, int c0,
-                                                uint32_t (&d)[20]) {
-    const int u = min(mfma4_split_unit(lg, first), units - 1);
+                                                uint32_t (&d)[4 * UnitParts<S>::kChunks]) {
+    const int u = min(mfma4_split_unit<S>(lg, first), units - 1);
     const int col = u >> lg, g = u & ((1 << lg) - 1);
     const QXT_GLOBAL v4u *src;
     if constexpr (LAYOUT == kLaneLayout) {
@@ -1117,7 +1118,7 @@ __device__ __forceinline__ void load_mfma4_half(const Q4Task &t, int col_base, i
               c0;
     }
 #pragma unroll
-    for (int v = 0; v < 5; ++v) {
+    for (int v = 0; v < UnitParts<S>::kChunks; ++v) {
         const v4u x = LAYOUT == kLaneLayout ? __builtin_nontemporal_load(src + v * kLaneGroup) : src[v];
         d[4 * v + 0] = x[0];
         d[4 * v + 1] = x[1];
@@ -1126,24 +1127,26 @@ __device__ __forceinline__ void load_mfma4_half(const Q4Task &t, int col_base, i
     }
 }
 
-template <int H>
-__device__ __forceinline__ void compute_mfma4_half(int lg, int units, int first, const uint32_t (&pr)[20],
-                                                   const int *aq, const int *ad, float *cb, const Q4Lds &geo,
-                                                   int cpw) {
+template <int S, int H>
+__device__ __forceinline__ void compute_mfma4_half(int lg, int units, int first,
+                                                   const uint32_t (&pr)[4 * UnitParts<S>::kChunks], const int *aq,
+                                                   const int *ad, float *cb, const Q4Lds &geo, int cpw) {
     typedef int v4i_t __attribute__((ext_vector_type(4)));
+    using Parts = UnitParts<S>;
+    constexpr int NB = Parts::kBlocks;
     const int lane = threadIdx.x & 63;
     const int b = lane >> 2, p = lane & 3;
     const int g = b & ((1 << lg) - 1);
     const int *arow = aq + p * geo.aq_row;
-    const int u = mfma4_split_unit(lg, first);
+    const int u = mfma4_split_unit<S>(lg, first);
     const int col = u >> lg;
     uint32_t d[36];  // the unit's words at their places (register renaming only)
 #pragma unroll
-    for (int k = 0; k < 20; ++k) d[16 * H + k] = pr[k];
-    float terms[4][4];
+    for (int k = 0; k < 4 * Parts::kChunks; ++k) d[4 * Parts::kChunkStep * H + k] = pr[k];
+    float terms[4][NB];
     auto do_block = [&](auto ic) {
         constexpr int i = decltype(ic)::value;
-        constexpr int I = 4 * H + i;
+        constexpr int I = NB * H + i;
         uint32_t sbits, qs[4];
         unit_block<I>(d, sbits, qs);
         const int bg = g * 8 + I;
@@ -1171,19 +1174,23 @@ __device__ __forceinline__ void compute_mfma4_half(int lg, int units, int first,
     };
     do_block(std::integral_constant<int, 0>{});
     do_block(std::integral_constant<int, 1>{});
-    do_block(std::integral_constant<int, 2>{});
-    do_block(std::integral_constant<int, 3>{});
+    if constexpr (NB == 4) {
+        do_block(std::integral_constant<int, 2>{});
+        do_block(std::integral_constant<int, 3>{});
+    }
     if (u < units) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            *reinterpret_cast<float4 *>(cb + (r * cpw + col) * geo.cbs + g * 8 + 4 * H) =
-                make_float4(terms[r][0], terms[r][1], terms[r][2], terms[r][3]);
+        for (int r = 0; r < 4; ++r) {
+            float *dst = cb + (r * cpw + col) * geo.cbs + g * 8 + NB * H;
+            if constexpr (NB == 4) *reinterpret_cast<float4 *>(dst) = make_float4(terms[r][0], terms[r][1], terms[r][2], terms[r][3]);
+            else *reinterpret_cast<float2 *>(dst) = make_float2(terms[r][0], terms[r][1]);
+        }
     }
 }
 
-template <int LAYOUT>
-__global__ __launch_bounds__(2 * kThreads) void q4_0_mfma4_split_kernel(Q4Task t) {
-    constexpr int MR = 4, NT = 2 * kThreads;
+template <int LAYOUT, int S>
+__global__ __launch_bounds__(S * kThreads) void q4_0_mfma4_split_kernel(Q4Task t) {
+    constexpr int MR = 4, NT = S * kThreads;
     extern __shared__ int lds[];
     const int col_base = blockIdx.x * t.cpw;
     const int r0 = blockIdx.y * MR;
@@ -1195,29 +1202,39 @@ __global__ __launch_bounds__(2 * kThreads) void q4_0_mfma4_split_kernel(Q4Task t
     const int tile_cols = min(t.cpw, t.ncols - col_base);
     const int G = B >> 3;
     const int units = tile_cols * G;
-    const int half = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)) & 1;
-    const int c0 = 4 * half;
+    const int part = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)) % S;
+    const int c0 = UnitParts<S>::kChunkStep * part;
     Q8RowRegs<NT> a;
     fetch_q8_rows(t, r0, a);
     __builtin_amdgcn_sched_barrier(0);  // keep the activation loads first
     const int lg = __builtin_ctz(G);
-    constexpr int R = NT / 2;  // units per round: two waves per unit
-    uint32_t wr[20], wn[20];
-    load_mfma4_half<LAYOUT>(t, col_base, lg, units, 0, c0, wr);
-    load_mfma4_half<LAYOUT>(t, col_base, lg, units, R, c0, wn);
+    constexpr int R = NT / S;  // units per round: S waves per unit
+    constexpr int W = 4 * UnitParts<S>::kChunks;
+    uint32_t wr[W], wn[W];
+    load_mfma4_half<LAYOUT, S>(t, col_base, lg, units, 0, c0, wr);
+    load_mfma4_half<LAYOUT, S>(t, col_base, lg, units, R, c0, wn);
     __builtin_amdgcn_sched_barrier(0);
     stage_q8_rows(t, a, aq, ad, geo);
     __syncthreads();
-    auto compute = [&](int first, const uint32_t (&pr)[20]) {
-        if (half == 0) compute_mfma4_half<0>(lg, units, first, pr, aq, ad, cb, geo, t.cpw);
-        else compute_mfma4_half<1>(lg, units, first, pr, aq, ad, cb, geo, t.cpw);
+    auto compute = [&](int first, const uint32_t (&pr)[W]) {
+        if constexpr (S == 2) {
+            if (part == 0) compute_mfma4_half<2, 0>(lg, units, first, pr, aq, ad, cb, geo, t.cpw);
+            else compute_mfma4_half<2, 1>(lg, units, first, pr, aq, ad, cb, geo, t.cpw);
+        } else {
+            switch (part) {
+                case 0: compute_mfma4_half<4, 0>(lg, units, first, pr, aq, ad, cb, geo, t.cpw); break;
+                case 1: compute_mfma4_half<4, 1>(lg, units, first, pr, aq, ad, cb, geo, t.cpw); break;
+                case 2: compute_mfma4_half<4, 2>(lg, units, first, pr, aq, ad, cb, geo, t.cpw); break;
+                default: compute_mfma4_half<4, 3>(lg, units, first, pr, aq, ad, cb, geo, t.cpw); break;
+            }
+        }
     };
     for (int first = 0;;) {
         compute(first, wr);
-        load_mfma4_half<LAYOUT>(t, col_base, lg, units, first + 2 * R, c0, wr);
+        load_mfma4_half<LAYOUT, S>(t, col_base, lg, units, first + 2 * R, c0, wr);
         if ((first += R) >= units) break;
         compute(first, wn);
-        load_mfma4_half<LAYOUT>(t, col_base, lg, units, first + 2 * R, c0, wn);
+        load_mfma4_half<LAYOUT, S>(t, col_base, lg, units, first + 2 * R, c0, wn);
         if ((first += R) >= units) break;
     }
     __syncthreads();
@@ -1279,6 +1296,10 @@ constexpr bool kWideSplit = QXT_WIDE_SPLIT != 0;
 #define QXT_MFMA4_SPLIT 1
 #endif
 constexpr bool kMfma4Split = QXT_MFMA4_SPLIT != 0;
+#ifndef QXT_MFMA4_SPLIT_WAVES
+#define QXT_MFMA4_SPLIT_WAVES 2
+#endif
+constexpr int kMfma4SplitWaves = QXT_MFMA4_SPLIT_WAVES;
 
 #ifndef QXT_SPLIT_SINGLE
 #define QXT_SPLIT_SINGLE 1
@@ -1360,13 +1381,14 @@ int launch_single(Q4Task t, hipStream_t stream) {
             {
                 // Tiles of several rounds: each unit over two waves of 512
                 // (measured on MI355X, cfg2 back to back: N = 11008, three
-                // rounds, 9.7 -> 9.3 us; N = 4096, one round, 5.5 -> 5.65 us,
-                // so single-round tiles keep one wave per unit).
+                // rounds, 9.7 -> 9.3 us, and 10.1 us over four waves of 1024;
+                // N = 4096, one round, 5.5 -> 5.65 us, so single-round tiles
+                // keep one wave per unit).
                 if (kMfma4Split && t.cpw * G > kMfma4Threads)
-                    return t.lanes ? launch(name, q4_0_mfma4_split_kernel<kLaneLayout>, grid, dim3(2 * kThreads), lds,
-                                            stream, t)
-                                   : launch(name, q4_0_mfma4_split_kernel<kNativeRows>, grid, dim3(2 * kThreads),
-                                            lds, stream, t);
+                    return t.lanes ? launch(name, q4_0_mfma4_split_kernel<kLaneLayout, kMfma4SplitWaves>, grid,
+                                            dim3(kMfma4SplitWaves * kThreads), lds, stream, t)
+                                   : launch(name, q4_0_mfma4_split_kernel<kNativeRows, kMfma4SplitWaves>, grid,
+                                            dim3(kMfma4SplitWaves * kThreads), lds, stream, t);
                 return t.lanes ? launch(name, q4_0_mfma4_kernel<kLaneLayout, kMfma4Threads>, grid,
                                         dim3(kMfma4Threads), lds, stream, t)
                                : launch(name, q4_0_mfma4_kernel<kNativeRows, kMfma4Threads>, grid,
