@@ -621,14 +621,14 @@ struct FusedRows {
 };
 
 // Load fp32 row r of the fused path into xv (zeros past K).
-template <int RC>
+template <int RC, int NT = kThreads>
 __device__ __forceinline__ void load_row(const GemmArgs &args, const FusedRows &f, int r, v4u (&xv)[RC]) {
     const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(f.x, f.x_bytes);
     const int k4 = args.k / 4;
     const uint32_t base = static_cast<uint32_t>(r) * f.ldx;
 #pragma unroll
     for (int u = 0; u < RC; ++u) {
-        const int c = threadIdx.x + u * kThreads;
+        const int c = threadIdx.x + u * NT;
         xv[u] = __builtin_amdgcn_raw_buffer_load_b128(rx, c < k4 ? base + c * 16 : kOutOfRange, 0, 0);
     }
 }
@@ -638,13 +638,13 @@ __device__ __forceinline__ void load_row(const GemmArgs &args, const FusedRows &
 // the epilogue reads from args.sa).  Fused rows: row 0 arrives in `xv0`,
 // which the caller loaded (before its weight loads, so that waiting for the
 // row does not wait for them); later rows are loaded here.
-template <int MR, int RC, bool FUSED>
+template <int MR, int RC, bool FUSED, int NT = kThreads>
 __device__ __forceinline__ void stage_rows(const GemmArgs &args, const FusedRows &f, v4u *act, float *row_sa,
                                            float *scratch, const v4u (&xv0)[RC]) {
     const int k16 = args.k / 16;
     if constexpr (!FUSED) {
         const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(args.a, args.a_bytes);
-        for (int i = threadIdx.x; i < MR * k16; i += kThreads) {
+        for (int i = threadIdx.x; i < MR * k16; i += NT) {
             const int r = i / k16, c = i - r * k16;
             const uint32_t off = r < args.m ? static_cast<uint32_t>(r) * args.lda + c * 16 : kOutOfRange;
             act[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
@@ -656,7 +656,7 @@ __device__ __forceinline__ void stage_rows(const GemmArgs &args, const FusedRows
         const int k4 = args.k / 4;
         for (int r = 0; r < MR; ++r) {
             if (r >= args.m) {
-                for (int c = threadIdx.x; c < k4; c += kThreads) aw[r * k4 + c] = 0;
+                for (int c = threadIdx.x; c < k4; c += NT) aw[r * k4 + c] = 0;
                 continue;
             }
             // The row is read once into registers, reduced, then quantised from them.
@@ -665,7 +665,7 @@ __device__ __forceinline__ void stage_rows(const GemmArgs &args, const FusedRows
 #pragma unroll
                 for (int u = 0; u < RC; ++u) xv[u] = xv0[u];
             } else {
-                load_row<RC>(args, f, r, xv);
+                load_row<RC, NT>(args, f, r, xv);
             }
             float amax = 0.0f;
 #pragma unroll
@@ -676,7 +676,9 @@ __device__ __forceinline__ void stage_rows(const GemmArgs &args, const FusedRows
             for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
             if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = amax;
             __syncthreads();
-            amax = fmaxf(fmaxf(scratch[0], scratch[1]), fmaxf(scratch[2], scratch[3]));
+            amax = scratch[0];
+#pragma unroll
+            for (int w = 1; w < NT / 64; ++w) amax = fmaxf(amax, scratch[w]);
             __syncthreads();  // scratch is reused by the next row
             const float sc = row_scale(amax, f.floor != 0);
             // Through the scale's reciprocal, as rows_int8_kernel.
@@ -688,7 +690,7 @@ __device__ __forceinline__ void stage_rows(const GemmArgs &args, const FusedRows
             };
 #pragma unroll
             for (int u = 0; u < RC; ++u) {
-                const int c = threadIdx.x + u * kThreads;
+                const int c = threadIdx.x + u * NT;
                 if (c >= k4) break;
                 const v4u v = xv[u];
                 const uint32_t word = pack_bytes(quant(v[0]), quant(v[1]), quant(v[2]), quant(v[3]));
@@ -715,22 +717,23 @@ __device__ __forceinline__ void stage_rows(const GemmArgs &args, const FusedRows
 // eight-kilobyte ring for long rows was no faster).  A wave sum per column
 // ends it.
 constexpr int kNonTemporal = 2;  // buffer-load cache policy bits: nt
-constexpr int kGemvColsNK = 16;  // per workgroup: 4 waves x 4 columns
-template <int MR, int RC, int EPI, bool FUSED>
-__global__ __launch_bounds__(kThreads) void w8a8_gemv_nk_kernel(GemmArgs args, FusedRows f) {
+constexpr int kGemvColsNK = 16;  // per workgroup: 4 waves x 4 columns, or 8 waves x 2
+template <int MR, int RC, int EPI, bool FUSED, int NT = kThreads>
+__global__ __launch_bounds__(NT) void w8a8_gemv_nk_kernel(GemmArgs args, FusedRows f) {
+    constexpr int CPW = kGemvColsNK / (NT / 64);  // columns per wave
     extern __shared__ v4u act[];  // [MR][K / 16]
     __shared__ float row_sa[4];
-    __shared__ float scratch[kThreads / 64];
+    __shared__ float scratch[NT / 64];
     const int k16 = args.k / 16;
     const int lane = threadIdx.x & 63;
-    const int n0 = blockIdx.x * kGemvColsNK + (threadIdx.x >> 6) * 4;
+    const int n0 = blockIdx.x * kGemvColsNK + (threadIdx.x >> 6) * CPW;
     const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(args.w, args.w_bytes);
-    uint32_t row_off[4];
+    uint32_t row_off[CPW];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) row_off[j] = n0 + j < args.n ? static_cast<uint32_t>(n0 + j) * args.ldw : kOutOfRange;
-    auto load_cols = [&](v4u (&v)[4], int c) {
+    for (int j = 0; j < CPW; ++j) row_off[j] = n0 + j < args.n ? static_cast<uint32_t>(n0 + j) * args.ldw : kOutOfRange;
+    auto load_cols = [&](v4u (&v)[CPW], int c) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < CPW; ++j)
             v[j] = __builtin_amdgcn_raw_buffer_load_b128(
                 rb, row_off[j] == kOutOfRange || c >= k16 ? kOutOfRange : row_off[j] + c * 16, 0, kNonTemporal);
     };
@@ -738,14 +741,14 @@ __global__ __launch_bounds__(kThreads) void w8a8_gemv_nk_kernel(GemmArgs args, F
     // c0 + 64 d of the current group of 256 chunks.
     constexpr int kDepth = 4;
     v4u xv0[RC];
-    if constexpr (FUSED) load_row<RC>(args, f, 0, xv0);
-    v4u ring[kDepth][4];
+    if constexpr (FUSED) load_row<RC, NT>(args, f, 0, xv0);
+    v4u ring[kDepth][CPW];
 #pragma unroll
     for (int d = 0; d < kDepth; ++d) load_cols(ring[d], lane + 64 * d);
-    stage_rows<MR, RC, FUSED>(args, f, act, row_sa, scratch, xv0);
-    int acc[4][MR];
+    stage_rows<MR, RC, FUSED, NT>(args, f, act, row_sa, scratch, xv0);
+    int acc[CPW][MR];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < CPW; ++j)
 #pragma unroll
         for (int r = 0; r < MR; ++r) acc[j][r] = 0;
     for (int c0 = lane; c0 < k16; c0 += 64 * kDepth) {
@@ -757,7 +760,7 @@ __global__ __launch_bounds__(kThreads) void w8a8_gemv_nk_kernel(GemmArgs args, F
                 for (int r = 0; r < MR; ++r) {
                     const v4u av = act[r * k16 + c];
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
+                    for (int j = 0; j < CPW; ++j) {
                         int sum = acc[j][r];
                         sum = dot4(static_cast<int>(ring[d][j][0]), static_cast<int>(av[0]), sum);
                         sum = dot4(static_cast<int>(ring[d][j][1]), static_cast<int>(av[1]), sum);
@@ -771,12 +774,12 @@ __global__ __launch_bounds__(kThreads) void w8a8_gemv_nk_kernel(GemmArgs args, F
         }
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < CPW; ++j)
 #pragma unroll
         for (int r = 0; r < MR; ++r) acc[j][r] = wave_sum(acc[j][r]);
     if (lane == 0) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < CPW; ++j)
 #pragma unroll
             for (int r = 0; r < MR; ++r)
                 if (n0 + j < args.n && r < args.m) store_one<EPI>(args, r, n0 + j, acc[j][r], row_sa[r]);
@@ -876,7 +879,7 @@ int launch_stream(const GemmArgs &args, int epi, hipStream_t stream) {
     return launch("w8a8_gemm_stream_kernel", kernel, grid, dim3(big::THREADS), 0, stream, a2);
 }
 
-template <int MR, int RC, bool FUSED>
+template <int MR, int RC, bool FUSED, int NT = kThreads>
 int launch_gemv_rc(GemmArgs args, const FusedRows &f, int epi, uint32_t layout, hipStream_t stream) {
     args.a_bytes = static_cast<uint32_t>(static_cast<size_t>(args.m - 1) * args.lda + args.k);
     const size_t lds = static_cast<size_t>(MR) * args.k;
@@ -889,18 +892,32 @@ int launch_gemv_rc(GemmArgs args, const FusedRows &f, int epi, uint32_t layout, 
                       stream, args, f);
     }
     args.w_bytes = static_cast<uint32_t>(static_cast<size_t>(args.n - 1) * args.ldw + args.k);
-    auto kernel = epi == EPI_I32        ? w8a8_gemv_nk_kernel<MR, RC, EPI_I32, FUSED>
-                  : epi == EPI_DEQUANT ? w8a8_gemv_nk_kernel<MR, RC, EPI_DEQUANT, FUSED>
-                                       : w8a8_gemv_nk_kernel<MR, RC, EPI_DEQUANT_BIAS, FUSED>;
-    return launch("w8a8_gemv_kernel", kernel, dim3((args.n + kGemvColsNK - 1) / kGemvColsNK), dim3(kThreads), lds,
-                  stream, args, f);
+    auto kernel = epi == EPI_I32        ? w8a8_gemv_nk_kernel<MR, RC, EPI_I32, FUSED, NT>
+                  : epi == EPI_DEQUANT ? w8a8_gemv_nk_kernel<MR, RC, EPI_DEQUANT, FUSED, NT>
+                                       : w8a8_gemv_nk_kernel<MR, RC, EPI_DEQUANT_BIAS, FUSED, NT>;
+    return launch("w8a8_gemv_kernel", kernel, dim3((args.n + kGemvColsNK - 1) / kGemvColsNK), dim3(NT), lds, stream,
+                  args, f);
 }
 
-// Fused rows are held as K / 1024 chunks per thread, rounded up to 4, 8 or 16
-// (fewer registers for short rows, more workgroups per CU).
+// Fused rows are held as K / (4 * threads) chunks per thread, rounded up to
+// 4, 8 or 16 (fewer registers for short rows, more workgroups per CU).  The
+// [N, K] weights run 512-thread workgroups of eight waves with two columns
+// each: every thread then holds half as much of the row, so the workgroup's
+// quantisation, which no weight can be reduced before, ends sooner
+// (measured on MI355X, cfg4 at M = 1 with rotated weights: down 16.4 ->
+// 14.9-15.1 us, gate_up 15.5-15.9 -> 15.2-15.3 us event-timed).
+#ifndef QXT_GEMV_WIDE
+#define QXT_GEMV_WIDE 1
+#endif
+constexpr bool kGemvWide = QXT_GEMV_WIDE != 0;
 template <int MR, bool FUSED>
 int launch_gemv(const GemmArgs &args, const FusedRows &f, int epi, uint32_t layout, hipStream_t stream) {
     if constexpr (FUSED) {
+        if (kGemvWide && layout == QXT_W8A8_WEIGHT_NK) {
+            constexpr int NT = 2 * kThreads;
+            if (args.k <= 4 * 4 * NT) return launch_gemv_rc<MR, 4, true, NT>(args, f, epi, layout, stream);
+            return launch_gemv_rc<MR, 8, true, NT>(args, f, epi, layout, stream);
+        }
         if (args.k <= 4 * 4 * kThreads) return launch_gemv_rc<MR, 4, true>(args, f, epi, layout, stream);
         if (args.k <= 8 * 4 * kThreads) return launch_gemv_rc<MR, 8, true>(args, f, epi, layout, stream);
         return launch_gemv_rc<MR, kGemvRowChunks, true>(args, f, epi, layout, stream);
