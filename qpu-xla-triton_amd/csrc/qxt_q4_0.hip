@@ -1484,7 +1484,7 @@ struct qxt_q4_0_batch {
     int prefetch = 0;  // activation chunks per thread prefetched (every task one fp32 row), or 0
     int upt = 1;       // units per thread of the batch kernel
     int split = 1;     // waves per unit (one-row prefetch batches of narrow items)
-    bool wide = false; // 512-thread workgroups (split 2 or 4)
+    int threads = kThreads;  // 256, or 512 / 1024 for split prefetch batches
     size_t lds = 0;
     bool in_args = false;  // tasks and items travel in the kernel arguments
     Q4ArgBatch args{};
@@ -1515,10 +1515,10 @@ BatchKernel batch_kernel_for(int layout) {
 // One-row prefetch batches.  split: waves per unit; wide: 512-thread
 // workgroups (the row's chunks over twice the threads).
 template <int U, int PC>
-BatchKernel prefetch_kernel_split(int layout, int split, bool wide) {
+BatchKernel prefetch_kernel_split(int layout, int split, int threads) {
     if constexpr (U == 1) {
-        if (wide && split == 4) return batch_kernel_for<1, 1, (PC + 1) / 2, 4, 2 * kThreads>(layout);
-        if (wide) return batch_kernel_for<1, 1, (PC + 1) / 2, 2, 2 * kThreads>(layout);
+        if (threads == 2 * kThreads && split == 4) return batch_kernel_for<1, 1, (PC + 1) / 2, 4, 2 * kThreads>(layout);
+        if (threads == 2 * kThreads) return batch_kernel_for<1, 1, (PC + 1) / 2, 2, 2 * kThreads>(layout);
         if (split == 4) return batch_kernel_for<1, 1, PC, 4>(layout);
         if (split == 2) return batch_kernel_for<1, 1, PC, 2>(layout);
     }
@@ -1526,22 +1526,22 @@ BatchKernel prefetch_kernel_split(int layout, int split, bool wide) {
 }
 
 template <int U>
-BatchKernel prefetch_kernel(int layout, int prefetch, int split, bool wide) {
+BatchKernel prefetch_kernel(int layout, int prefetch, int split, int threads) {
     switch (prefetch) {
-        case 2: return prefetch_kernel_split<U, 2>(layout, split, wide);
-        case 4: return prefetch_kernel_split<U, 4>(layout, split, wide);
-        default: return prefetch_kernel_split<U, kMaxPrefetchChunks>(layout, split, wide);
+        case 2: return prefetch_kernel_split<U, 2>(layout, split, threads);
+        case 4: return prefetch_kernel_split<U, 4>(layout, split, threads);
+        default: return prefetch_kernel_split<U, kMaxPrefetchChunks>(layout, split, threads);
     }
 }
 
 // The kernel of a batch: rows per task group, weight layout, activation
 // chunks prefetched per thread (0: none), units per thread and waves per
 // unit.
-BatchKernel batch_kernel(int mr, int layout, int prefetch, int upt, int split, bool wide) {
+BatchKernel batch_kernel(int mr, int layout, int prefetch, int upt, int split, int threads) {
     if (mr != 1) return batch_kernel_for<4, units_per_thread(4), 0>(layout);
     if (prefetch == 0) return batch_kernel_for<1, units_per_thread(1), 0>(layout);
-    return upt == 1 ? prefetch_kernel<1>(layout, prefetch, split, wide)
-                    : prefetch_kernel<units_per_thread(1)>(layout, prefetch, split, wide);
+    return upt == 1 ? prefetch_kernel<1>(layout, prefetch, split, threads)
+                    : prefetch_kernel<units_per_thread(1)>(layout, prefetch, split, threads);
 }
 
 }  // namespace
@@ -1898,9 +1898,13 @@ int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_
         // eight waves and each thread quantises half as many row chunks
         // (measured on MI355X, the staged decode of cfg3, gate/up and down
         // items of 176 units: 0.384 -> 0.374 ms; q/k/v items of 88 units over
-        // four of eight waves instead of two of four: 0.364 -> 0.361 ms).
-        batch->wide = kWideSplit && batch->split < 4;
-        if (batch->wide) batch->split = std::min(4, 2 * batch->split);
+        // four of eight waves instead of two of four: 0.364 -> 0.361 ms;
+        // 1024-thread workgroups for the 176-unit items, four waves per unit:
+        // 0.376 -> 0.383 ms).
+        if (kWideSplit && batch->split < 4) {
+            batch->threads = 2 * kThreads;
+            batch->split = std::min(4, 2 * batch->split);
+        }
     }
     batch->lds = lds;
     if (kArgBatches && count <= static_cast<uint32_t>(kArgTasks)) {
@@ -1927,8 +1931,8 @@ int qxt_q4_0_batch_launch(const qxt_q4_0_batch *batch, void *stream) {
         if (rc != QXT_OK) return rc;
     }
     const BatchKernel kernel =
-        batch_kernel(batch->mr, batch->layout, batch->prefetch, batch->upt, batch->split, batch->wide);
-    const dim3 block(batch->wide ? 2 * kThreads : kThreads);
+        batch_kernel(batch->mr, batch->layout, batch->prefetch, batch->upt, batch->split, batch->threads);
+    const dim3 block(batch->threads);
     if (batch->in_args)
         return launch("q4_0_batch_kernel", kernel.args, dim3(batch->grid), block, batch->lds, as_stream(stream),
                       batch->args);
