@@ -847,8 +847,10 @@ __global__ __launch_bounds__(kThreads) void q4_0_linear_kernel(Q4Task t) {
 // compile-time choice: under a run-time branch the compiler cannot count
 // the weight loads issued after it and waits for all of them.
 //
-// S > 1 (one-row prefetch batches of at most 64 * (NT / 64) / S units per
-// item, NT = 256 or 512 threads): each unit is split over S waves.  Wave w
+// S > 1 (one-row tiles of at most 64 * (NT / 64) / S units, NT = 256 or 512
+// threads: the items of prefetching batches, whose fp32 row is quantised in
+// the workgroup, and single linears over a native Q8_0 row): each unit is
+// split over S waves.  Wave w
 // takes part w % S -- blocks [8/S * part, +8/S) -- of units 64 * (w / S) +
 // lane, loading only the 16-byte chunks that hold them, so each wave's share
 // of the block dots is 1/S of a unit instead of a whole unit on fewer lanes.
