@@ -1399,8 +1399,10 @@ int launch_single(Q4Task t, hipStream_t stream) {
         if constexpr (MR == 1) {
             const int units = t.cpw * G;
             if (kSplitSingle && fast && t.x == nullptr && t.blocks <= 512 && units <= 4 * kLaneGroup) {
-                // Tiles of at most 64 units: 4 waves of 256 threads per unit;
-                // more: 512 threads, 4 (up to 128 units) or 2 waves per unit.
+                // Tiles of at most 64 units: 4 waves of 256 threads per unit
+                // (512 threads measured 0.5 % slower on the per-linear decode
+                // schedule); more: 512 threads, 4 (up to 128 units) or 2
+                // waves per unit.
                 if (units <= kLaneGroup)
                     return t.lanes ? launch(name, q4_0_split_kernel<kLaneLayout, 4, kThreads>, grid, dim3(kThreads),
                                             lds, stream, t)
@@ -1895,15 +1897,16 @@ int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_
         int max_units = 0;
         for (const Q4Task &t : host) max_units = std::max(max_units, t.cpw * (t.blocks / 8));
         batch->split = max_units <= kLaneGroup ? 4 : max_units <= 2 * kLaneGroup ? 2 : 1;
-        // Items of more than 64 units: 512-thread workgroups, so that a unit
-        // still splits over two (129-256 units) or four (65-128) of their
-        // eight waves and each thread quantises half as many row chunks
-        // (measured on MI355X, the staged decode of cfg3, gate/up and down
-        // items of 176 units: 0.384 -> 0.374 ms; q/k/v items of 88 units over
-        // four of eight waves instead of two of four: 0.364 -> 0.361 ms;
-        // 1024-thread workgroups for the 176-unit items, four waves per unit:
-        // 0.376 -> 0.383 ms).
-        if (kWideSplit && batch->split < 4) {
+        // 512-thread workgroups, so that a unit still splits over two
+        // (129-256 units) or four (up to 128) of their eight waves and each
+        // thread quantises half as many row chunks (measured on MI355X, the
+        // staged decode of cfg3, gate/up and down items of 176 units: 0.384
+        // -> 0.374 ms; q/k/v items of 88 units over four of eight waves
+        // instead of two of four: 0.364 -> 0.361 ms; o items of 64 units,
+        // half the waves idle during the block terms: 0.370 -> 0.368 ms;
+        // 1024-thread workgroups for the 176-unit items, four waves per
+        // unit: 0.376 -> 0.383 ms).
+        if (kWideSplit) {
             batch->threads = 2 * kThreads;
             batch->split = std::min(4, 2 * batch->split);
         }
