@@ -76,6 +76,8 @@ def test_reference_seed_fixture_bit_exact_and_block_dots() -> None:
         (6, 16, 130),     # four-row matrix-core tiles over native rows, two block ranges per unit
         (4, 32, 77),      # four block ranges per unit
         (4, 64, 9000),    # eight block ranges per unit, tiles of several rounds
+        (1, 448, 300),    # K=14336 at one row: split units over 512 threads, 448 Q8_0 blocks fetched
+        (1, 512, 200),    # K=16384: the largest row the split single linear fetches into registers
     ],
 )
 def test_random_shapes_bit_exact(rows: int, blocks: int, outputs: int) -> None:
