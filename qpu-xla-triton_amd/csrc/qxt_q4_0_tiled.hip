@@ -12,9 +12,12 @@
 // and is checked against the oracle within rtol 2e-6; this kernel matches
 // the oracle exactly.)
 //
-// The four VALU operations per output and block (convert, two multiplies,
-// add) are the kernels' floor, not the matrix core: one 32 x 32 x 32 MFMA per
-// wave per block feeds 64 VALU instructions.  A 256-thread workgroup owns a
+// The VALU operations per output and block (convert, two multiplies, add)
+// are the kernels' floor, not the matrix core: one 32 x 32 x 32 MFMA per wave
+// per block feeds the scaling of 16 outputs per lane.  Where registers allow
+// (the split planes, and the staged kernel's small grids), the MFMA's
+// accumulator input is a bias that makes the convert and the first multiply
+// one fma (see kDotBiasBits): three instructions per output and block.  A 256-thread workgroup owns a
 // 64 x 64 output tile (four waves of 32 x 32), and the dots of the next block
 // are computed before the current block's are scaled.  Two operand layouts,
 // two ways of feeding the matrix core:
@@ -109,12 +112,116 @@ __device__ __forceinline__ void frags_of(const RawFrags &f, v4i &a, v4i &w) {
 constexpr int kAhead = 4;  // blocks of fragments in flight ahead of the one being reduced
 static_assert(kAhead % 2 == 0 && kChunk % kAhead == 0, "block parity must be static in the unrolled loop");
 
+// Biased block dots.  The MFMA's accumulator input is the bit pattern of
+// 1.5 * 2^23 in every output, so an output's bits are those of the float
+// f = 1.5 * 2^23 + dot (|dot| <= 32 * 128 * 128 = 2^19 < 2^22 keeps it among
+// that binade's integers).  Then fl32(float(dot) * dw) = fma(f, dw, c) with
+// c = -1.5 * 2^23 * dw, exactly: c is exact (dw is an fp16 value, 11
+// significant bits) and the fma rounds f * dw + c = dot * dw once.  For
+// dot * dw = 0 the fma gives +0 where the product may be -0; the accumulator
+// starts at +0 and so never holds -0, and adding either zero leaves it
+// unchanged.  An infinite or NaN dw makes c non-finite, so the kernels note
+// every non-finite weight scale they stage, and a workgroup that staged one
+// computes its tile again with exact_terms_split / exact_terms_native.
+constexpr int kDotBiasBits = 0x4B400000;
+constexpr float kDotBias = 12582912.0f;
+
+__device__ __forceinline__ v16i dot_bias() {
+    v16i v;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) v[r] = kDotBiasBits;
+    return v;
+}
+
+__device__ __forceinline__ bool half_bits_finite(uint32_t bits16) { return (bits16 & 0x7C00u) != 0x7C00u; }
+
+// Row of output r (0..15) of a lane: the 32 x 32 MFMA's output layout.
+__device__ __forceinline__ int out_row(int mbase, int r) { return mbase + 8 * (r >> 2) + (r & 3); }
+
+// The exact per-block form, c_b = fl32(fl32(float(dot) * dw) * da) summed in
+// block order, for one lane's 16 outputs (rows out_row(mbase, r), column bn),
+// straight from the split planes in global memory (v_dot4 per 4 k), one
+// output at a time so that it needs few registers.  Only for workgroups
+// whose weight scales are not all finite.
+__device__ __forceinline__ void exact_terms_split(const TiledArgs &t, int mbase, int bn, float (&acc)[16]) {
+    const __amdgpu_buffer_rsrc_t ra = rsrc(t.aq, t.a_extent);
+    const __amdgpu_buffer_rsrc_t rw = rsrc(t.wq, t.w_extent);
+    const __amdgpu_buffer_rsrc_t ras = rsrc(t.as, t.as_extent);
+    const __amdgpu_buffer_rsrc_t rws = rsrc(t.ws, t.ws_extent);
+    const bool n_ok = bn < t.n;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int m = out_row(mbase, r);
+        const bool m_ok = m < t.m;
+        float sum = 0.0f;
+#pragma unroll 1
+        for (int b = 0; b < t.blocks; ++b) {
+            const uint32_t ao = m_ok ? static_cast<uint32_t>(m) * t.aq_stride + b * 32 : kOutOfRange;
+            const uint32_t wo = n_ok ? static_cast<uint32_t>(b * 8) * t.wq_stride + bn * 4 : kOutOfRange;
+            int dot = 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                dot = dot4(static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(ra, ao + 4 * j, 0, 0)),
+                           static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(rw, wo + j * t.wq_stride, 0, 0)), dot);
+            const float dw = half_bits_to_float(__builtin_amdgcn_raw_buffer_load_b16(
+                rws, n_ok ? static_cast<uint32_t>(b) * t.ws_stride + bn * 2 : kOutOfRange, 0, 0));
+            const float da = half_bits_to_float(__builtin_amdgcn_raw_buffer_load_b16(
+                ras, m_ok ? static_cast<uint32_t>(m) * t.as_stride + b * t.as_bytes : kOutOfRange, 0, 0));
+            sum = sum + (static_cast<float>(dot) * dw) * da;
+        }
+        acc[r] = sum;
+    }
+}
+
+// The same from native 34-byte Q8_0 / 18-byte Q4_0 blocks (2-byte aligned:
+// 16-bit loads).  Byte j of a Q4_0 block's nibbles holds element j (low) and
+// j + 16 (high), each minus 8.
+__device__ __forceinline__ void exact_terms_native(const TiledArgs &t, int mbase, int bn, float (&acc)[16]) {
+    const __amdgpu_buffer_rsrc_t ra = rsrc(t.act, t.a_extent);
+    const __amdgpu_buffer_rsrc_t rw = rsrc(t.w, t.w_extent);
+    const bool n_ok = bn < t.n;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int m = out_row(mbase, r);
+        const bool m_ok = m < t.m;
+        float sum = 0.0f;
+#pragma unroll 1
+        for (int b = 0; b < t.blocks; ++b) {
+            const uint32_t wo = n_ok ? static_cast<uint32_t>(t.wcol0 + bn) * t.w_stride + b * 18u : kOutOfRange;
+            const uint32_t ao = m_ok ? static_cast<uint32_t>(m) * t.act_stride + b * 34u : kOutOfRange;
+            int dot = 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t nib = __builtin_amdgcn_raw_buffer_load_b16(rw, wo + 2 + 2 * j, 0, 0);
+                const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(ra, ao + 2 + 2 * j, 0, 0);   // k = 2j, 2j+1
+                const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(ra, ao + 18 + 2 * j, 0, 0);  // k = 2j+16, 2j+17
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const uint32_t byte = (nib >> (8 * e)) & 0xFFu;
+                    dot += static_cast<int8_t>(lo >> (8 * e)) * (static_cast<int>(byte & 0xFu) - 8);
+                    dot += static_cast<int8_t>(hi >> (8 * e)) * (static_cast<int>(byte >> 4) - 8);
+                }
+            }
+            const float dw = half_bits_to_float(__builtin_amdgcn_raw_buffer_load_b16(rw, wo, 0, 0));
+            const float da = half_bits_to_float(__builtin_amdgcn_raw_buffer_load_b16(ra, ao, 0, 0));
+            sum = sum + (static_cast<float>(dot) * dw) * da;
+        }
+        acc[r] = sum;
+    }
+}
+
 // COLUMN: the column-scale variant (the llama.cpp bridge's COLUMN_W8 weight
 // mode): int8 weights with one fp32 scale per column instead of fp16 block
 // scales; each block adds fl32(float(dot) * da) and the column scale
 // multiplies the finished sum once (ggml_q4_0.py:497-525).
+// The block-scale form needs more than 168 registers either way, so it is
+// compiled for at most two waves per SIMD: left to itself the scheduler kept
+// one 16-register dot buffer and scaled each block right after its MFMA,
+// waiting on the matrix core (M = 512 down projection 45.9 us against 42.8 us
+// with the dots of the next block in flight).
 template <bool COLUMN>
-__global__ __launch_bounds__(kThreads) void q4_0_tiled_kernel(TiledArgs t) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, COLUMN ? 8 : 2))) void q4_0_tiled_kernel(
+    TiledArgs t) {
     // Scales of two chunks: the one being reduced and the next, written
     // while the current one is reduced (one barrier per chunk).
     __shared__ __attribute__((aligned(16))) float s_da[2][kChunk][kTile];
@@ -136,7 +243,10 @@ __global__ __launch_bounds__(kThreads) void q4_0_tiled_kernel(TiledArgs t) {
     float acc[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
-    const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    // Biased dots for the block-scale form; the column-scale form has no dw
+    // and converts plain dots.
+    const v16i cin = COLUMN ? v16i{} : dot_bias();
+    bool finite = true;  // every weight scale this thread staged
 
     // Ring of fragment registers: slot j holds block b with b % kAhead == j.
     // The dots of block b + 1 are computed (`next`) before block b's dots are
@@ -151,7 +261,7 @@ __global__ __launch_bounds__(kThreads) void q4_0_tiled_kernel(TiledArgs t) {
     {
         v4i af, wf;
         frags_of(ring[0], af, wf);
-        dots[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, wf, zero, 0, 0, 0);
+        dots[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, wf, cin, 0, 0, 0);
         issue_frags(t, ra, rw, base, kAhead, ring[0]);
     }
 
@@ -179,7 +289,10 @@ __global__ __launch_bounds__(kThreads) void q4_0_tiled_kernel(TiledArgs t) {
             const int i = threadIdx.x + u * kThreads;
             const int cb = i / kTile, r = i - cb * kTile;
             s_da[buf][cb][r] = half_bits_to_float(da_bits[u]);
-            if constexpr (!COLUMN) s_dw[buf][cb][r] = half_bits_to_float(dw_bits[u]);
+            if constexpr (!COLUMN) {
+                s_dw[buf][cb][r] = half_bits_to_float(dw_bits[u]);
+                finite = finite && half_bits_finite(dw_bits[u]);
+            }
         }
     };
     load_scales(0);
@@ -215,18 +328,22 @@ __global__ __launch_bounds__(kThreads) void q4_0_tiled_kernel(TiledArgs t) {
                     const int jn = (j + 1) % kAhead;
                     v4i af, wf;
                     frags_of(ring[jn], af, wf);
-                    dots[(j + 1) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, wf, zero, 0, 0, 0);
+                    dots[(j + 1) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, wf, cin, 0, 0, 0);
                     issue_frags(t, ra, rw, base, c0 + cb + 1 + kAhead, ring[jn]);
                 }
                 const v16i &d = dots[j & 1];
                 const float dw = COLUMN ? 1.0f : gdw[j];
+                const float c = dw * -kDotBias;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const float das[4] = {gda[j][q].x, gda[j][q].y, gda[j][q].z, gda[j][q].w};
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        float v = static_cast<float>(d[4 * q + e]);
-                        if constexpr (!COLUMN) v = v * dw;
+                        float v;
+                        if constexpr (COLUMN)
+                            v = static_cast<float>(d[4 * q + e]);
+                        else
+                            v = fmaf(__int_as_float(d[4 * q + e]), dw, c);
                         v = v * das[e];
                         acc[4 * q + e] = acc[4 * q + e] + v;
                     }
@@ -238,6 +355,9 @@ __global__ __launch_bounds__(kThreads) void q4_0_tiled_kernel(TiledArgs t) {
         store_scales(buf ^ 1);
         load_scales(c0 + 2 * kChunk);
         __syncthreads();
+    }
+    if constexpr (!COLUMN) {
+        if (__syncthreads_or(!finite)) exact_terms_split(t, m0 + wm * 32 + 4 * h, bn, acc);
     }
     if (!b_ok) return;
     const float cs = COLUMN ? t.cs[bn] : 1.0f;
@@ -365,7 +485,9 @@ __device__ __forceinline__ void stage_load(const TiledArgs &t, __amdgpu_buffer_r
     }
 }
 
-__device__ __forceinline__ void stage_store(const StageRegs &r, StageBuf &s) {
+// Returns whether every weight scale this thread staged is finite.
+__device__ __forceinline__ bool stage_store(const StageRegs &r, StageBuf &s) {
+    bool finite = true;
 #pragma unroll
     for (int q = 0; q < kPairs; ++q) {
         int row, jb;
@@ -394,11 +516,14 @@ __device__ __forceinline__ void stage_store(const StageRegs &r, StageBuf &s) {
         dst[0] = v4u{lo[0], lo[1], lo[2], lo[3]};
         dst[1] = v4u{hi[0], hi[1], hi[2], hi[3]};
         s.dw[jb][col] = half_bits_to_float(r.dw[q]);
+        finite = finite && half_bits_finite(r.dw[q]);
     }
+    return finite;
 }
 
 template <bool SELECT>
-__global__ __launch_bounds__(kThreads) void q4_0_staged_kernel(TiledArgs t) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, SELECT ? 8 : 2))) void q4_0_staged_kernel(
+    TiledArgs t) {
     __shared__ __attribute__((aligned(16))) StageBuf stage[2];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
@@ -414,11 +539,18 @@ __global__ __launch_bounds__(kThreads) void q4_0_staged_kernel(TiledArgs t) {
     float acc[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
-    const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    // Grids of two or more workgroups per CU need this kernel at three
+    // workgroups per CU (at most 168 registers): there (SELECT) the dots stay
+    // plain int32 and are converted.  The bias would cost 16 registers (214
+    // VGPRs, two workgroups per CU: gate_up at M = 512 38.5 -> 43.3 us);
+    // smaller grids run one or two workgroups per CU and take it (down at
+    // M = 512 48.4 -> 46.4 us).
+    constexpr bool BIASED = !SELECT;
+    const v16i cin = BIASED ? dot_bias() : v16i{};
 
     StageRegs regs;
     stage_load<SELECT>(t, ra, rw, m0, n0, 0, regs);
-    stage_store(regs, stage[0]);
+    bool finite = stage_store(regs, stage[0]);
     stage_load<SELECT>(t, ra, rw, m0, n0, kGroup, regs);
     __syncthreads();
 
@@ -437,7 +569,7 @@ __global__ __launch_bounds__(kThreads) void q4_0_staged_kernel(TiledArgs t) {
         {
             v4i a, w;
             frag(s, 0, a, w);
-            dots[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, w, zero, 0, 0, 0);
+            dots[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, w, cin, 0, 0, 0);
         }
 #pragma unroll
         for (int half = 0; half < kGroup; half += 4) {
@@ -456,15 +588,17 @@ __global__ __launch_bounds__(kThreads) void q4_0_staged_kernel(TiledArgs t) {
                 if (jb + 1 < kGroup) {
                     v4i a, w;
                     frag(s, jb + 1, a, w);
-                    dots[(jb + 1) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, w, zero, 0, 0, 0);
+                    dots[(jb + 1) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, w, cin, 0, 0, 0);
                 }
                 const v16i &d = dots[jb & 1];
+                const float c = gdw[j] * -kDotBias;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const float das[4] = {gda[j][q].x, gda[j][q].y, gda[j][q].z, gda[j][q].w};
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        float v = static_cast<float>(d[4 * q + e]) * gdw[j];
+                        float v = BIASED ? fmaf(__int_as_float(d[4 * q + e]), gdw[j], c)
+                                         : static_cast<float>(d[4 * q + e]) * gdw[j];
                         v = v * das[e];
                         acc[4 * q + e] = acc[4 * q + e] + v;
                     }
@@ -473,9 +607,12 @@ __global__ __launch_bounds__(kThreads) void q4_0_staged_kernel(TiledArgs t) {
         }
         // The other buffer was last read a group ago (before the previous
         // barrier): fill it with the next group and load the one after.
-        stage_store(regs, stage[buf ^ 1]);
+        finite = stage_store(regs, stage[buf ^ 1]) && finite;
         stage_load<SELECT>(t, ra, rw, m0, n0, g0 + 2 * kGroup, regs);
         __syncthreads();
+    }
+    if constexpr (BIASED) {
+        if (__syncthreads_or(!finite)) exact_terms_native(t, m0 + wm * 32 + 4 * h, bn, acc);
     }
     if (bn >= t.n) return;
 #pragma unroll

@@ -419,6 +419,55 @@ def test_native_linear_prefill_rows_run_on_matrix_cores_bit_exact(rows: int, blo
     np.testing.assert_array_equal(out[:, 16:], oracle.q4_0_q8_0_reference(act, wt[wcol0:wcol0 + ncols]))
 
 
+def _extreme_scale_case(rows: int, blocks: int, outputs: int):
+    """Scales at and past the ends of fp16 and dots of zero, placed in the first
+    two 64-column tiles only: the other tiles keep finite scales throughout."""
+    rng = np.random.default_rng(77)
+    da = rng.uniform(0.001, 0.2, (rows, blocks)).astype(np.float16)
+    av = rng.integers(-127, 128, (rows, blocks, 32))
+    dw = rng.uniform(-0.2, 0.2, (outputs, blocks)).astype(np.float16)
+    codes = rng.integers(0, 16, (outputs, blocks, 32))
+    dw[3, 1] = np.inf       # dot * inf: +-inf, or NaN where the dot is 0
+    dw[70, 0] = -np.inf
+    dw[5, 2] = np.nan
+    dw[7, :] = 65504.0
+    dw[8, :] = -65504.0
+    dw[9, :] = np.float16(2.0**-24)  # smallest fp16 subnormal
+    dw[10, :] = 0.0
+    dw[11, :] = -0.0
+    dw[12, :] = -0.125
+    codes[12] = 8                    # weight values 0: every dot of column 12 is 0
+    av[2, 1] = 0                     # row 2, block 1: every dot is 0 (0 * inf in column 3)
+    da[4, 0] = np.inf                # an infinite activation scale against finite dw
+    da[6, 2] = 65504.0
+    av[6, 2] = 127
+    act = oracle.pack_q8_0_blocks(da, av)
+    wt = oracle.pack_q4_0_blocks(dw, codes)
+    with np.errstate(invalid="ignore", over="ignore"):
+        expected = oracle.q4_0_q8_0_reference(act, wt)
+    assert np.isnan(expected[2, 3]) and np.isinf(expected[:, 3]).any() and np.isnan(expected[:, 5]).all()
+    assert np.isfinite(expected[np.ix_([0, 1, 3, 5], range(128, outputs))]).all()
+    return act, wt, expected
+
+
+@pytest.mark.parametrize("layout", ["native", "split"])
+def test_prefill_non_finite_and_extreme_block_scales_bit_exact(layout: str) -> None:
+    # The prefill kernels read block dots biased by 1.5 * 2^23 through one fma
+    # per output when every weight scale of the workgroup's tile is finite,
+    # and compute a tile again in the exact conversion form when one is not:
+    # both forms against the oracle, NaN where the oracle gives NaN.
+    rows, blocks, outputs = 40, 3, 200
+    act, wt, expected = _extreme_scale_case(rows, blocks, outputs)
+    if layout == "native":
+        out = torch.full((rows, outputs), float(SENTINEL), device="cuda")
+        q4.ggml_q4_0_q8_0_linear(dev(act), dev(wt), out)
+    else:
+        wscales, wquants = q4.pack_ggml_q4_0_tiled_weights(dev(wt))
+        ascales, aquants = q4.split_ggml_q8_0_blocks(dev(act))
+        out = q4.ggml_q4_0_q8_0_tiled_linear(aquants, ascales, wquants, wscales)
+    np.testing.assert_array_equal(out.cpu().numpy(), expected)
+
+
 # ------------------------------------------------------------- lane layout
 
 
