@@ -541,10 +541,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, SEL
     for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
     // Grids of two or more workgroups per CU need this kernel at three
     // workgroups per CU (at most 168 registers): there (SELECT) the dots stay
-    // plain int32 and are converted.  The bias would cost 16 registers (214
-    // VGPRs, two workgroups per CU: gate_up at M = 512 38.5 -> 43.3 us);
-    // smaller grids run one or two workgroups per CU and take it (down at
-    // M = 512 48.4 -> 46.4 us).
+    // plain int32 and are converted.  The bias costs 16 registers (measured
+    // at M = 512 gate_up: 169 VGPRs, two workgroups per CU, 44.0 us; made to
+    // fit 168 by reading the activation scales two blocks at a time, 39.3 us;
+    // plain dots 38.3 us).  Smaller grids run one or two workgroups per CU and
+    // take it (down at M = 512 48.4 -> 46.4 us).
     constexpr bool BIASED = !SELECT;
     const v16i cin = BIASED ? dot_bias() : v16i{};
 
