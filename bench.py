@@ -75,7 +75,14 @@ def parse_args() -> argparse.Namespace:
 
 
 class Runner:
-    """Prebuilt ctypes calls on one stream, replayable eagerly or as a captured HIP graph."""
+    """Prebuilt ctypes calls on one stream, replayable eagerly or as a captured HIP graph.
+
+    The operands are made on torch's current stream, the launches go to
+    ``stream``: the first launch waits for the whole device (every producer
+    queued so far), and ``uses`` marks tensors as used on ``stream`` so the
+    caching allocator does not hand their blocks out again while launches on
+    it are pending.
+    """
 
     def __init__(self, torch, stream) -> None:
         from qpu_xla_amd import _lib
@@ -86,11 +93,22 @@ class Runner:
         self._lib = _lib
         self.calls: list[tuple[object, tuple]] = []
         self.handle = ctypes.c_void_p(int(stream.cuda_stream))
+        self._ordered = False
 
     def add(self, name: str, *args) -> None:
         self.calls.append((getattr(self.lib, name), args))
 
+    def uses(self, *tensors) -> None:
+        for t in tensors:
+            t.record_stream(self.stream)
+
+    def _order_after_producers(self) -> None:
+        if not self._ordered:
+            self.torch.cuda.synchronize()
+            self._ordered = True
+
     def run(self) -> None:
+        self._order_after_producers()
         for fn, args in self.calls:
             rc = fn(*args)
             if rc:
@@ -99,6 +117,7 @@ class Runner:
     def capture(self):
         torch = self.torch
         graph = torch.cuda.CUDAGraph()
+        self._order_after_producers()
         torch.cuda.synchronize()
         with torch.cuda.graph(graph, stream=self.stream):
             self.run()
@@ -126,6 +145,7 @@ class Runner:
         """One graph holding `steps` consecutive steps (each step's launches in order)."""
         torch = self.torch
         graph = torch.cuda.CUDAGraph()
+        self._order_after_producers()
         torch.cuda.synchronize()
         with torch.cuda.graph(graph, stream=self.stream):
             for _ in range(steps):
@@ -196,6 +216,29 @@ def _fp16_field(torch, blocks):
     return blocks[..., 0:2].contiguous().view(torch.float16)[..., 0].float()
 
 
+def _mismatch(torch, label: str, r: int, got, want, inputs: dict, others: dict | None = None) -> RuntimeError:
+    """The error for a failed check: which columns differ, their bits, and non-finite inputs.
+
+    NaN never equals NaN, so a NaN in an input (a bias, a scale) fails the
+    check even where the kernel computed the same NaN; the message says so.
+    ``others`` maps labels to outputs the differing columns are compared
+    with (another weight copy's result, say).
+    """
+    diff = (got != want).nonzero().flatten()
+    cols = diff[:8].tolist()
+    bits = lambda t, c: f"{int(t[c:c + 1].view(torch.int32)[0]) & 0xFFFFFFFF:08x}"  # noqa: E731
+    detail = ", ".join(f"col {c}: got {bits(got, c)} want {bits(want, c)}" for c in cols)
+    both_nan = int((torch.isnan(got) & torch.isnan(want)).sum())
+    nonfinite = {name: int((~torch.isfinite(t)).sum()) for name, t in inputs.items() if t is not None}
+    msg = (f"{label}: row {r}: {diff.numel()} of {want.numel()} outputs differ from the reference arithmetic "
+           f"({detail}; NaN in both at {both_nan} of them; non-finite inputs {nonfinite})")
+    for name, other in (others or {}).items():
+        same = int((other[diff] == got[diff]).sum())
+        msg += f"; {same} of the differing columns equal {name}"
+    log(msg)
+    return RuntimeError(msg)
+
+
 def check_q4_0(torch, label: str, q8_blocks, q4_blocks, output, rows=(0,)) -> dict:
     """output[r, :N] == sum_b fl32(fl32(float(dot_b) * dw) * da) in block order, for r in rows."""
     w = q4_blocks.cpu()
@@ -212,13 +255,16 @@ def check_q4_0(torch, label: str, q8_blocks, q4_blocks, output, rows=(0,)) -> di
             acc = acc + (dots[:, b].float() * dw[:, b]) * da[b]
         got = output[r, : w.shape[0]].cpu()
         if not torch.equal(got, acc):
-            bad = int((got != acc).sum())
-            raise RuntimeError(f"{label}: row {r}: {bad} of {acc.numel()} outputs differ from the reference arithmetic")
+            raise _mismatch(torch, label, r, got, acc, {"weight scales": dw, "activation scales": da})
     return {"rows_checked": list(rows), "columns": int(w.shape[0]), "bit_exact": True}
 
 
-def check_w8a8(torch, label: str, x, qa, sa, weight, bias, y, rows=(0,)) -> dict:
-    """Row quantiser (scale floor 1/127, rint of the true quotient) and acc*sa*sw + bias, bit for bit."""
+def check_w8a8(torch, label: str, x, qa, sa, weight, bias, y, rows=(0,), others: dict | None = None) -> dict:
+    """Row quantiser (scale floor 1/127, rint of the true quotient) and acc*sa*sw + bias, bit for bit.
+
+    ``others`` maps labels to other outputs [M, N] (another weight copy's
+    result, say) that a mismatch report compares the differing columns with.
+    """
     values = weight.values.cpu().to(torch.int64)
     sw = weight.scales.cpu()
     b = None if bias is None else bias.cpu()
@@ -233,9 +279,10 @@ def check_w8a8(torch, label: str, x, qa, sa, weight, bias, y, rows=(0,)) -> dict
         want = (acc * scale) * sw
         if b is not None:
             want = want + b
-        if not torch.equal(y[r].cpu(), want):
-            bad = int((y[r].cpu() != want).sum())
-            raise RuntimeError(f"{label}: row {r}: {bad} of {want.numel()} outputs differ from the reference arithmetic")
+        got = y[r].cpu()
+        if not torch.equal(got, want):
+            raise _mismatch(torch, label, r, got, want, {"x": xr, "column scales": sw, "bias": b},
+                            {name: o[r].cpu() for name, o in (others or {}).items()})
     return {"rows_checked": list(rows), "columns": int(sw.numel()), "bit_exact": True}
 
 
@@ -537,6 +584,7 @@ def leg_w8a8(torch, args, shapes: dict | None = None) -> dict:
         y = torch.empty((m, n), dtype=torch.float32, device="cuda")
         stream = torch.cuda.Stream()
         runner = Runner(torch, stream)
+        runner.uses(x, qa, sa, weight.values, weight.scales, bias, y)
         runner.add("qxt_w8a8_linear", _p(x), _rs(x), _p(qa), _rs(qa), _p(sa), _p(weight.values),
                    _rs(weight.values), _p(weight.scales), _p(bias), _p(y), _rs(y), m, n, k, 0, 0, runner.handle)
         runner.run()
@@ -624,9 +672,12 @@ def leg_w8a8_gemv(torch, args) -> dict:
         bias = torch.randn((n,), generator=gen, device="cuda") * 0.1
         qa = torch.empty((1, k), dtype=torch.int8, device="cuda")
         sa = torch.empty((1,), dtype=torch.float32, device="cuda")
-        y = torch.empty((1, n), dtype=torch.float32, device="cuda")
+        # One output per weight copy, so each checked copy's result stands alone.
+        ys = [torch.empty((1, n), dtype=torch.float32, device="cuda") for _ in weights]
         runner = Runner(torch, torch.cuda.Stream())
-        for wt in weights:
+        runner.uses(x, bias, qa, sa, *ys)
+        for wt, y in zip(weights, ys):
+            runner.uses(wt.values, wt.scales)
             runner.add("qxt_w8a8_linear", _p(x), _rs(x), _p(qa), _rs(qa), _p(sa), _p(wt.values), _rs(wt.values),
                        _p(wt.scales), _p(bias), _p(y), _rs(y), 1, n, k, 0, 0, runner.handle)
         runner.run()
@@ -647,8 +698,13 @@ def leg_w8a8_gemv(torch, args) -> dict:
             "launches_per_call": sum(len(v) for v in times.values()) // (2 * copies),
         }
         torch.cuda.synchronize()
-        out[label]["check"] = check_w8a8(torch, f"w8a8 gemv {label}", x, qa, sa, weights[-1], bias, y)
-        del graph, weights
+        checked = sorted({0, copies // 2, copies - 1})
+        out[label]["check"] = {
+            f"copy_{j}": check_w8a8(torch, f"w8a8 gemv {label} copy {j}", x, qa, sa, weights[j], bias, ys[j],
+                                    others={f"copy {i}": ys[i] for i in checked if i != j})
+            for j in checked
+        }
+        del graph, weights, ys
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
     return out
@@ -683,6 +739,7 @@ def leg_prefill(torch, args) -> dict:
         y = torch.empty((rows, n), dtype=torch.float32, device="cuda")
         y_split = torch.empty((rows, n), dtype=torch.float32, device="cuda")
         runner = Runner(torch, torch.cuda.Stream())
+        runner.uses(xq, wq, y, a_values, a_scales, w_words, w_scales, y_split)
         runner.add("qxt_ggml_q4_0_q8_0_linear", _p(xq), _rs(xq), _p(wq), _rs(wq), _p(y), _rs(y),
                    rows, k // 32, 0, 0, n, runner.handle)
         runner.add("qxt_ggml_q4_0_q8_0_tiled_linear", _p(a_values), _rs(a_values), _p(a_scales), _rs(a_scales),
@@ -739,6 +796,7 @@ def leg_geglu(torch, args) -> dict:
         ]
         runner = Runner(torch, torch.cuda.Stream())
         for gate, up, q8 in sets:
+            runner.uses(gate, up, q8)
             runner.add("qxt_ggml_geglu_q8_0", _p(gate), _rs(gate), _p(up), _rs(up), _p(table), _p(q8), _rs(q8),
                        rows, k, runner.handle)
         runner.run()

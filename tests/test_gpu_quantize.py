@@ -180,3 +180,109 @@ def test_q4_0_weights_known_answer_blocks() -> None:
         np.testing.assert_array_equal(values[0, b].astype(np.int64) + 8, codes, err_msg=name)
         if scale_bits is not None:
             assert int(blocks[0, b, 0]) | (int(blocks[0, b, 1]) << 8) == scale_bits, name
+
+
+# ------------------------------------------------ known answers of tests/q8_0_kats.py
+
+
+def _q8_0_kat_row() -> tuple[np.ndarray, list[tuple[str, int, list[int]]]]:
+    """The Q8_0 known-answer blocks as one fp32 row [1, 32 B] and (name, fp16 scale bits, 32 codes) per block."""
+    import q8_0_kats
+
+    kats = q8_0_kats.q8_0_kat_blocks()
+    row = np.concatenate([values for _, values, _, _ in kats])[None, :].astype(np.float32)
+    return row, [(name, bits, q8_0_kats.expected_codes(codes, 32)) for name, _, bits, codes in kats]
+
+
+def _check_q8_0_blocks(blocks: np.ndarray, expected, scale_shift: int = 0) -> None:
+    """Blocks u8 [B, 34] hold the literal codes; their scales the literal fp16 bits (times 2^scale_shift)."""
+    for b, (name, bits, codes) in enumerate(expected):
+        got_bits = int(blocks[b, 0]) | (int(blocks[b, 1]) << 8)
+        want = float(np.array([bits], np.uint16).view(np.float16)[0]) * 2.0**scale_shift
+        assert got_bits == int(np.float16(want).view(np.uint16)), f"{name}: scale bits {got_bits:#06x}"
+        np.testing.assert_array_equal(blocks[b, 2:].view(np.int8).astype(np.int64), codes, err_msg=name)
+
+
+def test_q8_0_known_answer_blocks_bit_exact() -> None:
+    # Codes that separate x * fl32(1/d) from x / d, half-even from half-away
+    # rounding and the fp32 d from its fp16 rounding, as literals.
+    row, expected = _q8_0_kat_row()
+    _check_q8_0_blocks(quantize_q8_0(dev(row)).cpu().numpy()[0], expected)
+
+
+def test_rows_int8_known_answer_rows_bit_exact() -> None:
+    # True division at a non-unit scale (a reciprocal product changes four
+    # codes), half-even ties, the 1/127 floor and the mode without it.
+    import q8_0_kats
+
+    for name, row, floor, scale_bits, codes in q8_0_kats.row_kats():
+        q, s = quantize_rows_int8(dev(row[None, :]), floor=floor)
+        np.testing.assert_array_equal(q.cpu().numpy()[0].astype(np.int64),
+                                      q8_0_kats.expected_codes(codes, row.size), err_msg=name)
+        assert int(s.cpu().numpy().view(np.uint32)[0]) == scale_bits, name
+
+
+def _selector_q4_0_weights(blocks: int) -> np.ndarray:
+    """Q4_0 weights [32 B, B, 18], d = 1: column n picks element n % 32 of block n // 32 (code 9 = +1, else 0)."""
+    n = 32 * blocks
+    codes = np.full((n, blocks, 32), 8, np.int64)
+    codes[np.arange(n), np.arange(n) // 32, np.arange(n) % 32] = 9
+    return oracle.pack_q4_0_blocks(np.ones((n, blocks), np.float16), codes)
+
+
+def _selected(expected, rows: int) -> np.ndarray:
+    """y[r, n] = code of element n % 32 of block n // 32 times that block's fp16 scale (exact in fp32)."""
+    y = np.concatenate([np.asarray(codes, np.float32) * np.float32(np.array([bits], np.uint16).view(np.float16)[0])
+                        for _, bits, codes in expected])
+    return np.repeat(y[None, :], rows, axis=0)
+
+
+@pytest.mark.parametrize("path", ["prefetch_m1", "fused_m4", "prepass"])
+def test_batch_quantisers_known_answers_through_selector_weights(path: str) -> None:
+    # The Q4_0 batch kernels quantise fp32 activations to Q8_0 themselves
+    # (inside each workgroup, or in a pre-pass launch for large batches).
+    # Selector weights make every output one code times its block's fp16
+    # scale, so the literal codes and scales are read back exactly.
+    from qpu_xla_amd import _lib
+    from qpu_xla_amd.kernels import ggml_q4_0 as q4
+
+    row, expected = _q8_0_kat_row()
+    # The batch kernels take K % 256 == 0: the known-answer blocks twice over.
+    row, expected = np.concatenate([row, row], axis=1), expected + expected
+    rows = 4 if path == "fused_m4" else 1
+    x = dev(np.repeat(row, rows, axis=0))
+    blocks = row.shape[1] // 32
+    w = dev(_selector_q4_0_weights(blocks))
+    y = torch.full((rows, 32 * blocks), float("nan"), device="cuda")
+    tasks = [{"x": x, "weight": w, "destination": y}]
+    if path == "prepass":
+        # A filler linear of many column tiles pushes the batch past the
+        # in-workgroup limit, so the activations go through the pre-pass.
+        # (Its bytes are random codes with fp16 scales of 1/64; its output is not checked.)
+        rng = np.random.default_rng(5)
+        filler = rng.integers(0, 256, (65536, 64, 18), dtype=np.uint8)
+        filler[..., 0:2] = np.array([2.0**-6], np.float16).view(np.uint8)
+        tasks.append({"x": dev(rng.standard_normal((1, 2048), dtype=np.float32)), "weight": dev(filler),
+                      "destination": torch.empty((1, 65536), device="cuda")})
+    with q4.Q4_0LinearBatch(tasks) as batch:
+        assert (batch.work_items > 1024) == (path == "prepass")
+        with _lib.launch_timing() as timing:
+            batch.launch()
+            torch.cuda.synchronize()
+    names = [name for name, _ in timing.records]
+    assert names == (["q8_0_prepass_kernel", "q4_0_batch_kernel"] if path == "prepass" else ["q4_0_batch_kernel"])
+    np.testing.assert_array_equal(y.cpu().numpy(), _selected(expected, rows))
+
+
+def test_geglu_producer_known_answers() -> None:
+    # gate = 4.0, whose fp16 GELU entry is 4.0 exactly: v = fl32(4 up) = 4 up,
+    # so the producer's Q8_0 codes are the known answers of `up` and every
+    # scale is 4 times the known one.
+    from qpu_xla_amd.kernels.ggml_geglu_q8 import ggml_geglu_q8_0, ggml_gelu_fp16_table
+
+    table = ggml_gelu_fp16_table()
+    assert int(table.view(torch.int16)[0x4400]) & 0xFFFF == 0x4400
+    row, expected = _q8_0_kat_row()
+    gate = dev(np.full_like(row, 4.0))
+    blocks = ggml_geglu_q8_0(gate, dev(row)).cpu().numpy()[0]
+    _check_q8_0_blocks(blocks, expected, scale_shift=2)

@@ -389,3 +389,49 @@ def test_calibrated_auto_selects_the_fastest_exact_partition_axis() -> None:
         assert empty._gpu is None
         with pytest.raises(ValueError, match="no CPU reference fallback"):
             empty.execute(destination, dev(x), queue=Queue())
+
+
+@pytest.mark.parametrize("layout", ["nk", "k4n"])
+@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("k", [8192, 8208, 16384])
+def test_fused_rows_at_register_chunk_boundaries_bit_exact(layout: str, m: int, k: int) -> None:
+    # The fused row quantiser holds K / (4 NT) 16-byte chunks per thread: K =
+    # 8192 is the last K of 4 chunks on the 512-thread [N, K] kernel (and of 8
+    # on the 256-thread K4N kernel), 8208 the first of the next size, 16384
+    # fills 8 (16) chunks exactly.  (M = 4 at K = 16384 needs 64 KiB of rows
+    # and runs the two-kernel path.)  Each row starts with the known-answer
+    # row of tests/q8_0_kats.py, whose absmax is the row's absmax, so its
+    # codes and scale are checked against literals as well as the oracle.
+    import q8_0_kats
+    from qpu_xla_amd import _lib
+    from qpu_xla_amd._tensors import ptr, row_stride
+
+    name, kat, _, scale_bits, codes = q8_0_kats.row_kats()[0]
+    rng = np.random.default_rng(k + m)
+    n = 96
+    x = np.clip(rng.standard_normal((m, k), dtype=np.float32), -4.0, 4.0).astype(np.float32)
+    x[:, : kat.size] = kat
+    wf = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    qw, sw = oracle.quantize_per_output_channel_int8(wf)
+    bias = (rng.standard_normal(n, dtype=np.float32) * np.float32(0.1)).astype(np.float32)
+    if layout == "nk":
+        w_d, kind = dev(qw), _lib.WEIGHT_NK
+    else:
+        w_d, kind = words(np.ascontiguousarray(oracle.pack_int8_quads(qw).T)), _lib.WEIGHT_K4N
+    xd, sw_d, b_d = dev(x), dev(sw), dev(bias)
+    qa = torch.full((m, k), 99, dtype=torch.int8, device="cuda")
+    sa = torch.full((m,), -1.0, dtype=torch.float32, device="cuda")
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    _lib.call("qxt_w8a8_linear", ptr(xd), row_stride(xd), ptr(qa), row_stride(qa), ptr(sa), ptr(w_d), row_stride(w_d),
+              ptr(sw_d), ptr(b_d), ptr(y), row_stride(y), m, n, k, kind, 0, None)
+    torch.cuda.synchronize()
+    qa_ref, sa_ref = oracle.quantize_rows_int8(x)
+    got_q, got_s = qa.cpu().numpy(), sa.cpu().numpy()
+    np.testing.assert_array_equal(got_q, qa_ref)
+    np.testing.assert_array_equal(got_s, sa_ref)
+    for r in range(m):
+        np.testing.assert_array_equal(got_q[r, : kat.size].astype(np.int64),
+                                      q8_0_kats.expected_codes(codes, kat.size), err_msg=name)
+        assert int(got_s[r : r + 1].view(np.uint32)[0]) == scale_bits
+    expected = oracle.dequantize_epilogue(oracle.int8_gemm_i32(qa_ref, qw), sa_ref, sw, bias)
+    np.testing.assert_array_equal(y.cpu().numpy(), expected)

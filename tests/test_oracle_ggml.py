@@ -9,6 +9,7 @@ import pytest
 
 import oracle
 import q4_0_kats
+import q8_0_kats
 from conftest import load_golden
 
 
@@ -141,6 +142,50 @@ def test_q8_0_quantiser_rounds_half_to_even() -> None:
     x[0, :6] = [127.0, 2.5, 3.5, -2.5, -3.5, 0.5]  # absmax 127 -> d = 1, inv = 1
     _, codes = oracle.quantize_q8_0_split(x)
     np.testing.assert_array_equal(codes[0, :6], [127, 2, 4, -2, -4, 0])
+
+
+@pytest.mark.parametrize("kat", q8_0_kats.q8_0_kat_blocks(), ids=lambda k: k[0])
+def test_q8_0_quantiser_known_answer_blocks(kat) -> None:
+    # Literal codes and fp16 scale bits (tests/q8_0_kats.py gives the fp32
+    # quotient each literal rounds).
+    name, values, scale_bits, codes = kat
+    bits, got = oracle.quantize_q8_0_split(values[None, :])
+    assert int(bits[0, 0]) == scale_bits, f"{name}: fp16 scale bits {int(bits[0, 0]):#06x}"
+    np.testing.assert_array_equal(got[0].astype(np.int64), q8_0_kats.expected_codes(codes, 32), err_msg=name)
+
+
+@pytest.mark.parametrize("kat", q8_0_kats.q8_0_kat_blocks(), ids=lambda k: k[0])
+def test_q8_0_known_answers_agree_with_exact_arithmetic(kat) -> None:
+    name, values, scale_bits, codes = kat
+    d, exact = q8_0_kats.exact_q8_0(values)
+    assert exact == q8_0_kats.expected_codes(codes, 32), name
+    assert int(np.float16(float(d)).view(np.uint16)) == scale_bits, name
+
+
+def test_q8_0_known_answers_reject_the_plausible_mistakes() -> None:
+    # Dividing by d instead of multiplying by fl32(1/d), quantising with the
+    # fp16-rounded d, or rounding half away from zero each changes at least
+    # one literal code (checked in exact arithmetic, so the oracle cannot pass
+    # the known answers with any of these mistakes).
+    name, values, _, codes = q8_0_kats.q8_0_kat_blocks()[0]
+    want = q8_0_kats.expected_codes(codes, 32)
+    for mistake in ("divide", "fp16_scale", "half_away"):
+        _, wrong = q8_0_kats.exact_q8_0(values, **{mistake: True})
+        assert wrong != want, mistake
+    # ... and a signed maximum instead of |x| flips the scale's sign bit.
+    assert q8_0_kats.q8_0_kat_blocks()[1][2] & 0x8000 == 0
+
+
+def test_q8_0_quantiser_random_blocks_match_exact_arithmetic() -> None:
+    rng = np.random.default_rng(31)
+    x = rng.standard_normal((3, 256), dtype=np.float32) * np.float32(2.5)
+    x[1] *= np.float32(1e-4)
+    bits, codes = oracle.quantize_q8_0_split(x)
+    for r in range(x.shape[0]):
+        for b in range(x.shape[1] // 32):
+            d, exact = q8_0_kats.exact_q8_0(x[r, 32 * b : 32 * b + 32])
+            np.testing.assert_array_equal(codes[r, 32 * b : 32 * b + 32].astype(np.int64), exact)
+            assert int(bits[r, b]) == int(np.float16(float(d)).view(np.uint16))
 
 
 def test_q8_0_blocks_equal_split_form() -> None:

@@ -6,6 +6,7 @@ import numpy as np
 import pytest
 
 import oracle
+import q8_0_kats
 from conftest import load_golden
 
 
@@ -83,11 +84,38 @@ def test_row_quantiser_invariants_and_floor() -> None:
     assert np.all(err <= s[:, None] * 0.5000001)
 
 
-def test_row_quantiser_true_division_and_half_even() -> None:
+def test_row_quantiser_half_even_at_unit_scale() -> None:
+    # At scale 1 division and reciprocal agree; this pins only the rounding.
     x = np.array([[127.0, 2.5, 3.5, -2.5, -126.5, 0.5]], dtype=np.float32)
     q, s = oracle.quantize_rows_int8(x)
     assert s[0] == np.float32(1.0)
     np.testing.assert_array_equal(q[0], [127, 2, 4, -2, -126, 0])
+
+
+@pytest.mark.parametrize("kat", q8_0_kats.row_kats(), ids=lambda k: k[0])
+def test_row_quantiser_known_answer_rows(kat) -> None:
+    # Literal codes and scale bits at non-unit scales (tests/q8_0_kats.py
+    # gives the fp32 quotient each literal rounds).
+    name, row, floor, scale_bits, codes = kat
+    q, s = oracle.quantize_rows_int8(row[None, :], floor=floor)
+    assert int(s.view(np.uint32)[0]) == scale_bits, name
+    np.testing.assert_array_equal(q[0].astype(np.int64), q8_0_kats.expected_codes(codes, row.size), err_msg=name)
+    exact_s, exact = q8_0_kats.exact_row(row, floor=floor)
+    assert exact == q8_0_kats.expected_codes(codes, row.size), name
+    assert float(exact_s) == float(s[0]), name
+
+
+def test_row_known_answers_reject_the_plausible_mistakes() -> None:
+    # A reciprocal product instead of the true quotient, or half-away-from-zero
+    # rounding, changes at least one literal code of the separator row; the
+    # floor row's codes change without the floor.
+    name, row, floor, _, codes = q8_0_kats.row_kats()[0]
+    want = q8_0_kats.expected_codes(codes, row.size)
+    for mistake in ("reciprocal", "half_away"):
+        _, wrong = q8_0_kats.exact_row(row, floor=floor, **{mistake: True})
+        assert wrong != want, mistake
+    _, row, _, _, codes = q8_0_kats.row_kats()[1]
+    assert q8_0_kats.exact_row(row, floor=False)[1] != q8_0_kats.expected_codes(codes, row.size)
 
 
 def test_weight_scale_floor_is_active_at_baseline_shapes() -> None:
