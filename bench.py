@@ -1009,30 +1009,6 @@ def cpu_references_w8a8(budget_s: float) -> dict:
     return out
 
 
-def measured_floors(key: str) -> dict | None:
-    """Floor decomposition of a single-linear launch from the committed profile summary, if any."""
-    path = ROOT / "profiles" / "q4_0_linear_kernel_floors.json"
-    try:
-        with open(path) as fh:
-            data = json.load(fh)
-    except (OSError, ValueError):
-        return None
-    entry = data.get(key)
-    if not isinstance(entry, dict):
-        return None
-    return {**entry, "source": str(path.relative_to(ROOT))}
-
-
-def attach_floor(leg: dict, key: str) -> None:
-    """Add the launch's measured floors and this run's time relative to its weight-load floor."""
-    floors = measured_floors(key)
-    if floors is None or "kernel_avg_us" not in leg:
-        return
-    leg["floor"] = floors
-    leg["vs_weight_load_floor"] = leg["kernel_avg_us"] / floors["weight_loads_us"]
-    leg["vs_empty_kernel"] = leg["kernel_avg_us"] / floors["empty_kernel_us"]
-
-
 def measured_traffic(kernel: str) -> dict | None:
     """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH/WRITE summary, if any."""
     path = ROOT / "profiles" / f"{kernel}_cfg3_traffic.json"
@@ -1109,13 +1085,10 @@ def main() -> int:
     if "cfg0" in legs:
         log("leg cfg0 rotated")
         out["cfg0"] = leg_rotated_q4(torch, args, 1, 2048, 5632, 0)
-        attach_floor(out["cfg0"], "cfg0")
         log(f"cfg0: {out['cfg0']}")
     if "cfg2" in legs:
         log("leg cfg2 rotated")
         out["cfg2"] = [leg_rotated_q4(torch, args, 4, 4096, 11008, 2), leg_rotated_q4(torch, args, 4, 4096, 4096, 2)]
-        attach_floor(out["cfg2"][0], "cfg2_n11008")
-        attach_floor(out["cfg2"][1], "cfg2_n4096")
         # The same launches over the native ggml rows (the drop-in layout, no re-layout).
         out["cfg2_native_layout"] = [leg_rotated_q4(torch, args, 4, 4096, 11008, 2, "native"),
                                      leg_rotated_q4(torch, args, 4, 4096, 4096, 2, "native")]

@@ -86,6 +86,12 @@ const char *qxt_last_error(void);
 void qxt_set_failure_mask(uint32_t mask);
 uint32_t qxt_get_failure_mask(void);
 
+/* Number of device and pinned-host allocations the library has made in this
+ * process (hipMalloc / hipHostMalloc through its own code, successful calls
+ * only).  No counterpart in the reference: it lets a caller check that an
+ * entry point allocates nothing (qxt_w8a8_linear_noalloc). */
+uint64_t qxt_allocation_count(void);
+
 /* Properties of the current HIP device; replaces qpu_llama_context_capabilities
  * (qpu_llama_runtime.h:90-92). */
 int qxt_device_query(qxt_device_info *out);

@@ -32,6 +32,19 @@ inline bool aligned(const void *p, size_t bytes) {
 // Number of compute units of the current device (cached per device).
 int compute_units();
 
+// Every device and pinned-host allocation of the library goes through these;
+// they count successful calls (qxt_allocation_count).
+hipError_t counted_malloc(void **ptr, size_t bytes);
+hipError_t counted_host_malloc(void **ptr, size_t bytes);
+template <typename T>
+hipError_t device_malloc(T **ptr, size_t bytes) {
+    return counted_malloc(reinterpret_cast<void **>(ptr), bytes);
+}
+template <typename T>
+hipError_t pinned_host_malloc(T **ptr, size_t bytes) {
+    return counted_host_malloc(reinterpret_cast<void **>(ptr), bytes);
+}
+
 // Per-launch timing (qxt_timing_begin/end): when enabled on the calling
 // thread, launches record device-side start/stop events.
 bool timing_enabled();

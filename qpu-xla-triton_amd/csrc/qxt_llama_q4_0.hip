@@ -250,8 +250,8 @@ int upload_weights(qxt_llama_q4_0_linear *l, const qxt_llama_q4_0_linear_desc *d
     void *raw = nullptr;     // host bytes as uploaded, when they are not yet native rows
     void *native = nullptr;  // native rows, when they are not the final layout
     hipError_t err = hipSuccess;
-    if (repack) err = hipMalloc(&raw, bytes);
-    if (err == hipSuccess && (l->lanes || approximate)) err = hipMalloc(&native, bytes);
+    if (repack) err = qxt::device_malloc(&raw, bytes);
+    if (err == hipSuccess && (l->lanes || approximate)) err = qxt::device_malloc(&native, bytes);
     if (err != hipSuccess) {
         (void)hipFree(raw);
         return ctx->fail(QXT_ALLOCATION_FAILED, "weight staging: %s", hipGetErrorString(err));
@@ -426,19 +426,19 @@ extern "C" int qxt_llama_q4_0_linear_prepare(qxt_llama_context *context, const q
                              static_cast<size_t>(d->rows) * (k + approx_scales);
 
     DeviceScope scope(context->device);
-    hipError_t err = hipMalloc(&l->weight, l->weight_bytes);
+    hipError_t err = qxt::device_malloc(&l->weight, l->weight_bytes);
     if (err == hipSuccess && approximate) {
-        err = hipMalloc(reinterpret_cast<void **>(&l->column_scales),
+        err = qxt::device_malloc(&l->column_scales,
                         static_cast<size_t>(d->resident_column_count) * sizeof(float));
-        if (err == hipSuccess) err = hipMalloc(reinterpret_cast<void **>(&l->activation_q), static_cast<size_t>(d->rows) * k);
-        if (err == hipSuccess) err = hipMalloc(&l->activation_scales, static_cast<size_t>(d->rows) * approx_scales);
+        if (err == hipSuccess) err = qxt::device_malloc(&l->activation_q, static_cast<size_t>(d->rows) * k);
+        if (err == hipSuccess) err = qxt::device_malloc(&l->activation_scales, static_cast<size_t>(d->rows) * approx_scales);
     }
-    if (err == hipSuccess) err = hipMalloc(&l->activation, act_bytes);
-    if (err == hipSuccess) err = hipMalloc(&l->activation_packed, act_bytes);
-    if (err == hipSuccess) err = hipMalloc(reinterpret_cast<void **>(&l->output), out_bytes);
-    if (err == hipSuccess) err = hipHostMalloc(&l->host_activation, act_bytes, hipHostMallocDefault);
+    if (err == hipSuccess) err = qxt::device_malloc(&l->activation, act_bytes);
+    if (err == hipSuccess) err = qxt::device_malloc(&l->activation_packed, act_bytes);
+    if (err == hipSuccess) err = qxt::device_malloc(&l->output, out_bytes);
+    if (err == hipSuccess) err = qxt::pinned_host_malloc(&l->host_activation, act_bytes);
     if (err == hipSuccess)
-        err = hipHostMalloc(reinterpret_cast<void **>(&l->host_output), out_bytes, hipHostMallocDefault);
+        err = qxt::pinned_host_malloc(&l->host_output, out_bytes);
     if (err == hipSuccess) err = hipEventCreateWithFlags(&l->done, hipEventDisableTiming);
     if (err != hipSuccess) {
         release_buffers(l);

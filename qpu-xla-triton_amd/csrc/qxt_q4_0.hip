@@ -1846,8 +1846,8 @@ int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_
     const size_t item_bytes = round(sizeof(Q4Item) * items.size());
     const size_t job_bytes = round(sizeof(Q8Job) * jobs.size());
     const size_t bytes = task_bytes + item_bytes + job_bytes + sizeof(Q8Chunk) * chunks.size();
-    if (hipMalloc(&batch->device_tables, bytes) != hipSuccess ||
-        (staging_bytes > 0 && hipMalloc(&batch->q8_staging, staging_bytes) != hipSuccess)) {
+    if (device_malloc(&batch->device_tables, bytes) != hipSuccess ||
+        (staging_bytes > 0 && device_malloc(&batch->q8_staging, staging_bytes) != hipSuccess)) {
         if (batch->device_tables != nullptr) (void)hipFree(batch->device_tables);
         delete batch;
         return fail(QXT_ALLOCATION_FAILED, "q4_0 batch: hipMalloc of %zu + %zu bytes failed", bytes, staging_bytes);

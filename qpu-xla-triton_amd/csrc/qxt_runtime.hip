@@ -18,6 +18,7 @@ namespace {
 
 thread_local char g_last_error[512] = "";
 std::atomic<uint32_t> g_failure_mask{0};
+std::atomic<uint64_t> g_allocations{0};
 
 struct LaunchTiming {
     bool enabled = false;
@@ -78,6 +79,18 @@ void timing_record(const char *kernel_name, hipEvent_t start, hipEvent_t stop) {
     if (start != nullptr && stop != nullptr) g_timing.records.push_back({kernel_name, start, stop});
 }
 
+hipError_t counted_malloc(void **ptr, size_t bytes) {
+    const hipError_t err = hipMalloc(ptr, bytes);
+    if (err == hipSuccess) g_allocations.fetch_add(1, std::memory_order_relaxed);
+    return err;
+}
+
+hipError_t counted_host_malloc(void **ptr, size_t bytes) {
+    const hipError_t err = hipHostMalloc(ptr, bytes, hipHostMallocDefault);
+    if (err == hipSuccess) g_allocations.fetch_add(1, std::memory_order_relaxed);
+    return err;
+}
+
 int compute_units() {
     static std::mutex lock;
     static std::vector<int> cache;
@@ -122,6 +135,8 @@ const char *qxt_last_error(void) { return qxt::g_last_error; }
 void qxt_set_failure_mask(uint32_t mask) { qxt::g_failure_mask.store(mask, std::memory_order_relaxed); }
 
 uint32_t qxt_get_failure_mask(void) { return qxt::g_failure_mask.load(std::memory_order_relaxed); }
+
+uint64_t qxt_allocation_count(void) { return qxt::g_allocations.load(std::memory_order_relaxed); }
 
 int qxt_device_query(qxt_device_info *out) {
     if (out == nullptr) return qxt::fail(QXT_INVALID_ARGUMENT, "qxt_device_query: null output");

@@ -153,6 +153,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "qxt_last_error": (c_char_p, []),
     "qxt_set_failure_mask": (None, [_U]),
     "qxt_get_failure_mask": (_U, []),
+    "qxt_allocation_count": (c_uint64, []),
     "qxt_device_query": (c_int, [POINTER(DeviceInfo)]),
     "qxt_stream_wait": (c_int, [_P]),
     "qxt_timing_begin": (c_int, []),
@@ -270,6 +271,11 @@ def set_failure_mask(mask: int) -> None:
 
 def get_failure_mask() -> int:
     return int(load().qxt_get_failure_mask())
+
+
+def allocation_count() -> int:
+    """Device and pinned-host allocations the library has made in this process."""
+    return int(load().qxt_allocation_count())
 
 
 def device_info() -> DeviceInfo:

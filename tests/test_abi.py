@@ -235,3 +235,8 @@ def test_w8a8_linear_noalloc_rejects_sizes_beyond_its_workspace_before_launch() 
     assert status == _lib.INVALID_ARGUMENT and "static workspace" in _lib.last_error()
     status = lib.qxt_w8a8_linear_noalloc(FAKE, 64, FAKE, 16, FAKE, None, FAKE, 64, 4, 16, 24, 0, 0, None)
     assert status == _lib.INVALID_ARGUMENT and "multiple of 16" in _lib.last_error()
+
+
+def test_allocation_count_is_a_host_counter() -> None:
+    # Nothing in the host-only tests allocates device memory through the library.
+    assert _lib.allocation_count() == 0

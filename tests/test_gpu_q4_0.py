@@ -627,3 +627,19 @@ def test_one_row_fp32_stage_batches_with_activation_prefetch_bit_exact(shapes) -
                     torch.cuda.synchronize()
                 assert [name for name, _ in timing.records] == ["q4_0_batch_kernel"]
                 _check_batch(batch_tasks, expected)
+
+
+def test_batch_prepare_allocations_are_counted() -> None:
+    # The library counts its own device allocations (qxt_allocation_count):
+    # preparing a batch allocates its device tables, launching it does not.
+    from qpu_xla_amd import _lib
+
+    tasks, expected = _batch_case(41, [(1, 2048, 256, 0, 256)])
+    before = _lib.allocation_count()
+    with q4.Q4_0LinearBatch(tasks) as batch:
+        prepared = _lib.allocation_count()
+        assert prepared > before
+        batch.launch()
+        torch.cuda.synchronize()
+        assert _lib.allocation_count() == prepared
+    _check_batch(tasks, expected)
