@@ -6,6 +6,10 @@ class QpuXlaError(Exception):
     """Base class for all failures of this library."""
 
 
+class DeviceClosedError(QpuXlaError):
+    """Work was submitted to a queue that is closed."""
+
+
 class AllocationError(QpuXlaError):
     """A buffer allocation or layout is invalid."""
 
@@ -16,6 +20,10 @@ class DependencyError(QpuXlaError):
 
 class EventTimeoutError(QpuXlaError):
     """Waiting for an event exceeded its timeout."""
+
+
+class EventCancelledError(QpuXlaError):
+    """The awaited event was cancelled before it ran."""
 
 
 class KernelError(QpuXlaError):

@@ -241,36 +241,40 @@ class PreparedW8A8Linear:
             raise DependencyError("prepared W8A8 linear tensors must live on the plan device")
         return batch
 
-    def _staged(self, source: torch.Tensor) -> torch.Tensor:
-        """Source with padded K and dense rows (a copy into the plan buffer when needed).
+    def _staged(self, source: torch.Tensor) -> tuple[torch.Tensor, bool]:
+        """(rows the kernels read, whether ``source`` must first be copied into them).
 
-        Runs on the current stream; callers enter the queue's stream first.
+        Rows already dense with the padded K are read in place; otherwise they
+        are copied into the plan's source buffer (whose padding is zero).
         """
         if self.padded_features == self.features and rows_are_dense(source):
-            return source
-        staged = self._source[: source.shape[0]]
-        staged[:, : self.features].copy_(source)
-        return staged
+            return source, False
+        return self._source[: source.shape[0]], True
 
-    @staticmethod
-    def _record(queue: Queue, name: str) -> Event:
-        hip_event = torch.cuda.Event()
-        hip_event.record(queue.stream)
-        return Event(queue, name, "gpu", hip_event)
+    def _stage(self, staged: torch.Tensor, source: torch.Tensor) -> None:
+        """Copy ``source`` into the plan's source buffer, on the current stream."""
+        staged[:, : self.features].copy_(source)
 
     # ------------------------------------------------------------- execution
+    #
+    # Each step is one Queue.launch: it runs in the queue's order (held while
+    # host work submitted earlier is pending), its event carries the step's
+    # status and device timestamps, and a failure inside it fails the event.
 
     def execute(self, destination: torch.Tensor, source: torch.Tensor, *, queue: Queue, wait_for=()) -> Event:
         """Submit quantise + GEMM + epilogue; returns the completion event."""
         self._begin()
         self._bind(queue)
         self._check_io(destination, source)
-        queue.order_after_caller((destination, source))
-        queue._wait_dependencies(wait_for)
-        with torch.cuda.stream(queue.stream):
-            src = self._staged(source)
-            w8a8_linear(src, self.weight, self.bias, destination, workspace=(self._qa, self._sa), stream=queue)
-            self._last_event = self._record(queue, "gfx950.w8a8_linear")
+        src, copy = self._staged(source)
+
+        def issue() -> None:
+            with torch.cuda.stream(queue.stream):
+                if copy:
+                    self._stage(src, source)
+                w8a8_linear(src, self.weight, self.bias, destination, workspace=(self._qa, self._sa), stream=queue)
+
+        self._last_event = queue.launch("gfx950.w8a8_linear", issue, tensors=(destination, source), wait_for=wait_for)
         return self._last_event
 
     def execute_prepared(self, destination: torch.Tensor, *, batch: int, queue: Queue, wait_for=()) -> Event:
@@ -288,14 +292,16 @@ class PreparedW8A8Linear:
             raise ValueError("prepared W8A8 linear destination shape does not align")
         if destination.device != self.device:
             raise DependencyError("prepared W8A8 linear destination must live on the plan device")
-        queue.order_after_caller((destination,))
-        queue._wait_dependencies(wait_for)
-        with torch.cuda.stream(queue.stream):
-            w8a8_gemm_dequantize(
-                self._qa[:batch], self.weight.values, self._sa, self.weight.scales, self.bias, destination,
-                stream=queue,
-            )
-            self._last_event = self._record(queue, "gfx950.w8a8_gemm_dequantize")
+
+        def issue() -> None:
+            with torch.cuda.stream(queue.stream):
+                w8a8_gemm_dequantize(
+                    self._qa[:batch], self.weight.values, self._sa, self.weight.scales, self.bias, destination,
+                    stream=queue,
+                )
+
+        self._last_event = queue.launch("gfx950.w8a8_gemm_dequantize", issue, tensors=(destination,),
+                                        wait_for=wait_for)
         return self._last_event
 
     def execute_hybrid(
@@ -319,30 +325,32 @@ class PreparedW8A8Linear:
         if qpu_outputs <= 0 or qpu_outputs >= self.outputs or qpu_outputs % PARTITION_ALIGNMENT:
             raise ValueError("hybrid W8A8 qpu_outputs must be aligned and leave a non-empty tail")
         self._bind(qpu_queue, cpu_queue)
-        qpu_queue.order_after_caller((destination, source))
-        cpu_queue.order_after_caller((destination, source))
-        qpu_queue._wait_dependencies(wait_for)
-        cpu_queue._wait_dependencies(wait_for)
         split = int(qpu_outputs)
-        with torch.cuda.stream(qpu_queue.stream):
-            src = source
-            if not rows_are_dense(source):
-                src = self._source[:batch, : self.features]
-                src.copy_(source)
-            # The quantiser zero-fills the padded K columns of the workspace.
-            quantize_rows_int8(src, padded_columns=self.padded_features, out=self._qa, scales=self._sa, stream=qpu_queue)
-            quantized = self._record(qpu_queue, "gfx950.quantize_rows_int8")
-        cpu_queue._wait_dependencies((quantized,))
-        parts = ((qpu_queue, slice(0, split)), (cpu_queue, slice(split, self.outputs)))
-        for queue, cols in parts:
-            with torch.cuda.stream(queue.stream):
-                w8a8_gemm_dequantize(
-                    self._qa[:batch], self.weight.values[cols], self._sa, self.weight.scales[cols],
-                    None if self.bias is None else self.bias[cols], destination[:, cols], stream=queue,
-                )
-        tail = self._record(cpu_queue, "gfx950.w8a8_gemm_dequantize")
-        qpu_queue._wait_dependencies((tail,))
-        self._last_event = self._record(qpu_queue, "gfx950.w8a8_linear.hybrid_join")
+        src = source if rows_are_dense(source) else self._source[:batch, : self.features]
+
+        def quantize() -> None:
+            with torch.cuda.stream(qpu_queue.stream):
+                if src is not source:
+                    src.copy_(source)
+                # The quantiser zero-fills the padded K columns of the workspace.
+                quantize_rows_int8(src, padded_columns=self.padded_features, out=self._qa, scales=self._sa,
+                                   stream=qpu_queue)
+
+        def part(queue: Queue, cols: slice):
+            def issue() -> None:
+                with torch.cuda.stream(queue.stream):
+                    w8a8_gemm_dequantize(
+                        self._qa[:batch], self.weight.values[cols], self._sa, self.weight.scales[cols],
+                        None if self.bias is None else self.bias[cols], destination[:, cols], stream=queue,
+                    )
+            return issue
+
+        quantized = qpu_queue.launch("gfx950.quantize_rows_int8", quantize, tensors=(destination, source),
+                                     wait_for=wait_for)
+        qpu_queue.launch("gfx950.w8a8_gemm_dequantize", part(qpu_queue, slice(0, split)))
+        tail = cpu_queue.launch("gfx950.w8a8_gemm_dequantize", part(cpu_queue, slice(split, self.outputs)),
+                                tensors=(destination, source), wait_for=(quantized, *wait_for))
+        self._last_event = qpu_queue.launch("gfx950.w8a8_linear.hybrid_join", lambda: None, wait_for=(tail,))
         return self._last_event
 
     def execute_hybrid_rows(
@@ -366,24 +374,30 @@ class PreparedW8A8Linear:
         if qpu_rows <= 0 or qpu_rows >= batch or qpu_rows % PARTITION_ALIGNMENT:
             raise ValueError("hybrid W8A8 qpu_rows must be aligned and leave a non-empty tail")
         self._bind(qpu_queue, cpu_queue)
-        qpu_queue.order_after_caller((destination, source))
-        cpu_queue.order_after_caller((destination, source))
-        qpu_queue._wait_dependencies(wait_for)
-        cpu_queue._wait_dependencies(wait_for)
         split = int(qpu_rows)
-        with torch.cuda.stream(qpu_queue.stream):
-            src = self._staged(source)
-            if src is not source:
-                cpu_queue._wait_dependencies((self._record(qpu_queue, "gfx950.stage_source"),))
-        for queue, rows in ((qpu_queue, slice(0, split)), (cpu_queue, slice(split, batch))):
-            with torch.cuda.stream(queue.stream):
-                w8a8_linear(
-                    src[rows], self.weight, self.bias, destination[rows],
-                    workspace=(self._qa[rows], self._sa[rows]), stream=queue,
-                )
-        tail = self._record(cpu_queue, "gfx950.w8a8_linear")
-        qpu_queue._wait_dependencies((tail,))
-        self._last_event = self._record(qpu_queue, "gfx950.w8a8_linear.hybrid_join")
+        src, copy = self._staged(source)
+
+        def rows_of(queue: Queue, rows: slice):
+            def issue() -> None:
+                with torch.cuda.stream(queue.stream):
+                    w8a8_linear(src[rows], self.weight, self.bias, destination[rows],
+                                workspace=(self._qa[rows], self._sa[rows]), stream=queue)
+            return issue
+
+        ready = tuple(wait_for)
+        if copy:
+            # The staged copy is made once, on the first queue; the second waits for it.
+            def stage() -> None:
+                with torch.cuda.stream(qpu_queue.stream):
+                    self._stage(src, source)
+
+            ready = (qpu_queue.launch("gfx950.stage_source", stage, tensors=(destination, source),
+                                      wait_for=wait_for),)
+        qpu_queue.launch("gfx950.w8a8_linear", rows_of(qpu_queue, slice(0, split)), tensors=(destination, source),
+                         wait_for=ready)
+        tail = cpu_queue.launch("gfx950.w8a8_linear", rows_of(cpu_queue, slice(split, batch)),
+                                tensors=(destination, source), wait_for=ready)
+        self._last_event = qpu_queue.launch("gfx950.w8a8_linear.hybrid_join", lambda: None, wait_for=(tail,))
         return self._last_event
 
 

@@ -202,13 +202,13 @@ def test_kernel_contract_checks() -> None:
     q8 = torch.empty((4, 2, 34), dtype=torch.uint8, device="cuda")
     with Queue() as queue:
         with pytest.raises(KernelError, match="grid"):
-            queue.submit(geglu.GGML_GEGLU_Q8_0_KERNEL, (dev(gate), dev(up), q8, table), grid=(4, 2, 1))
+            queue.submit(geglu.GGML_GEGLU_Q8_0_KERNEL, (dev(gate), dev(up), q8, table), grid=(4, 2, 1)).wait()
         with pytest.raises(KernelError, match="contiguous"):
-            queue.submit(geglu.GGML_GEGLU_Q8_0_KERNEL, (dev(gate), dev(up), q8[:, :1], table), grid=(1, 4, 1))
+            queue.submit(geglu.GGML_GEGLU_Q8_0_KERNEL, (dev(gate), dev(up), q8[:, :1], table), grid=(1, 4, 1)).wait()
         with pytest.raises(KernelError, match="split"):
             queue.submit(geglu.GGML_GEGLU_Q8_0_SPLIT_KERNEL,
                          (dev(gate), dev(up), torch.empty((4, 2), dtype=torch.float32, device="cuda"),
-                          torch.empty((4, 64), dtype=torch.uint8, device="cuda"), table), grid=(2, 4, 1))
+                          torch.empty((4, 64), dtype=torch.uint8, device="cuda"), table), grid=(2, 4, 1)).wait()
     with pytest.raises(ValueError, match="gelu_table"):
         geglu.ggml_geglu_q8_0(dev(gate), dev(up), table[:100])
     with pytest.raises(ValueError):

@@ -8,7 +8,7 @@ import torch
 
 import oracle
 from conftest import load_golden
-from qpu_xla_amd import KernelError, Queue, _lib
+from qpu_xla_amd import EventStatus, KernelError, Queue, _lib
 from qpu_xla_amd.kernels import ggml_q4_0 as q4
 
 pytestmark = pytest.mark.gpu
@@ -126,16 +126,22 @@ def test_contract_errors_leave_destination_untouched() -> None:
     a, w = dev(act), dev(wt)
     destination = torch.full((4, 32), float(SENTINEL), device="cuda")
     with Queue() as queue:
+        # As the reference's worker does, a failed executor fails the event;
+        # wait() raises the KernelError and nothing reaches the stream.
+        failed = queue.submit(q4.GGML_Q4_0_Q8_0_LINEAR_KERNEL, (a, w, destination, 0, 0, 32), grid=(1, 1, 1))
         with pytest.raises(KernelError, match="grid"):
-            queue.submit(q4.GGML_Q4_0_Q8_0_LINEAR_KERNEL, (a, w, destination, 0, 0, 32), grid=(1, 1, 1))
+            failed.wait()
+        assert failed.status is EventStatus.FAILED and isinstance(failed.exception, KernelError)
         with pytest.raises(KernelError, match="aligned"):
-            queue.submit(q4.GGML_Q4_0_Q8_0_LINEAR_KERNEL, (a, w, destination, 8, 0, 16), grid=(1, 1, 1))
+            queue.submit(q4.GGML_Q4_0_Q8_0_LINEAR_KERNEL, (a, w, destination, 8, 0, 16), grid=(1, 1, 1)).wait()
         _lib.set_failure_mask(_lib.FAIL_SUBMISSION)
         try:
-            with pytest.raises(KernelError):
-                queue.submit(q4.GGML_Q4_0_Q8_0_LINEAR_KERNEL, (a, w, destination, 0, 0, 32), grid=(2, 1, 1))
+            injected = queue.submit(q4.GGML_Q4_0_Q8_0_LINEAR_KERNEL, (a, w, destination, 0, 0, 32), grid=(2, 1, 1))
         finally:
             _lib.set_failure_mask(_lib.FAIL_NONE)
+        with pytest.raises(KernelError):
+            injected.wait()
+        assert injected.status is EventStatus.FAILED
         queue.synchronize()
     np.testing.assert_array_equal(destination.cpu().numpy(), SENTINEL)
 

@@ -42,10 +42,10 @@ def test_m4_kernel_contract_with_resident_partition() -> None:
         np.testing.assert_array_equal(out[:, 16:], expected[:, 16:])
         with pytest.raises(KernelError, match="grid"):
             queue.submit(q8.GGML_Q8_0_Q8_0_LINEAR_M4_KERNEL, (dev(act), dev(wt), destination, 0, 0, 32),
-                         grid=(1, 1, 1))
+                         grid=(1, 1, 1)).wait()
         with pytest.raises(KernelError, match="M=4"):
             queue.submit(q8.GGML_Q8_0_Q8_0_LINEAR_M4_KERNEL, (dev(act[:3]), dev(wt), destination[:3], 0, 0, 32),
-                         grid=(2, 1, 1))
+                         grid=(2, 1, 1)).wait()
 
 
 @pytest.mark.parametrize("rows,blocks,n,wcol0,ncols", [
