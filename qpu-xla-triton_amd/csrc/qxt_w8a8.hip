@@ -21,6 +21,7 @@
 // exact integer sum does not depend on how the chunk is ordered) and receives
 // D[8 * (r / 4) + 4 * (l / 32) + r % 4][l % 32] in accumulator register r.
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 #include <vector>
@@ -448,11 +449,8 @@ static_assert(2 * STAGE >= kEpilogueLds, "the epilogue reuses the operand buffer
 // XCD runs together form a compact block whose A and B panels are shared
 // through that XCD's L2 instead of being fetched by every XCD.
 constexpr int kXcds = 8;
-__device__ __forceinline__ void xcd_tile(int pid, int tm, int tn, int gm, int &ty, int &tx) {
-    const int total = tm * tn;
-    const int per = total / kXcds, rem = total % kXcds;
-    const int xcd = pid % kXcds, local = pid / kXcds;
-    const int seq = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+// Position `seq` of the grouped tile order: gm tile rows at a time, column by column.
+__device__ __forceinline__ void grouped_tile(int seq, int tm, int tn, int gm, int &ty, int &tx) {
     const int group = seq / (gm * tn);
     const int first = group * gm;
     const int rows = min(gm, tm - first);
@@ -461,18 +459,27 @@ __device__ __forceinline__ void xcd_tile(int pid, int tm, int tn, int gm, int &t
     tx = in_group / rows;
 }
 
-template <int EPI>
-__global__ __launch_bounds__(big::THREADS) void w8a8_gemm_stream_kernel(GemmArgs args) {
+__device__ __forceinline__ void xcd_tile(int pid, int tm, int tn, int gm, int &ty, int &tx) {
+    const int total = tm * tn;
+    const int per = total / kXcds, rem = total % kXcds;
+    const int xcd = pid % kXcds, local = pid / kXcds;
+    const int seq = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+    grouped_tile(seq, tm, tn, gm, ty, tx);
+}
+
+// Main loop of the large-tile kernel: accumulates K stages [s0, s1) of the
+// output tile at (m0, n0) into `acc` (zeroed first).  Stage s + 2 is loaded
+// while stage s computes; past s1 the loads read bytes nobody uses (or, past
+// the operands, out of the descriptor range: zeros), so the loop body stays
+// one basic block.  On return every wave is past its last LDS write, but
+// waves may still read fragments: callers synchronise before reusing `smem`.
+__device__ __forceinline__ void big_mainloop(const GemmArgs &args, uint8_t *smem, int m0, int n0, int s0, int s1,
+                                             v16i (&acc)[big::TM][big::TN], bool zero = true) {
     using namespace big;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int wm = (wave & 3) >> 1;                    // 128-row half of the tile
     const int wcol = (wave & 1) * 128 + (wave >> 2) * 64;  // first of the wave's 64 columns
-    int ty, tx;
-    xcd_tile(blockIdx.x, (args.m + BM - 1) / BM, (args.n + BN - 1) / BN, 4, ty, tx);
-    const int m0 = ty * BM;
-    const int n0 = tx * BN;
     const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(args.a, args.a_bytes);
     const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(args.w, args.w_bytes);
     const uint32_t lda = static_cast<uint32_t>(args.lda), ldw = static_cast<uint32_t>(args.ldw);
@@ -483,13 +490,14 @@ __global__ __launch_bounds__(big::THREADS) void w8a8_gemm_stream_kernel(GemmArgs
     const uint32_t b_off = static_cast<uint32_t>(n0 + crow) * ldw + ccol;
     const int st_off = crow * ROW + ccol;
 
-    v16i acc[TM][TN];
+    if (zero) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
+            for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+    }
 
     const int a_lane = (wm * 128 + (lane & 31)) * ROW + (lane >> 5) * 16;
     const int b_lane = (wcol + (lane & 31)) * ROW + (lane >> 5) * 16;
@@ -517,22 +525,22 @@ __global__ __launch_bounds__(big::THREADS) void w8a8_gemm_stream_kernel(GemmArgs
     };
 
     v4u regs0[Q], regs1[Q];
-    const int stages = args.k / BKT;
+    const int k_first = s0 * BKT;
 #pragma unroll
-    for (int q = 0; q < Q; ++q) load_chunk(regs0[q], q, 0);
+    for (int q = 0; q < Q; ++q) load_chunk(regs0[q], q, k_first);
 #pragma unroll
-    for (int q = 0; q < Q; ++q) load_chunk(regs1[q], q, BKT);
+    for (int q = 0; q < Q; ++q) load_chunk(regs1[q], q, k_first + BKT);
 #pragma unroll
     for (int q = 0; q < Q; ++q) store_chunk(smem, regs0[q], q);
     __syncthreads();
     read_frags(smem, 0, 0);
 
-    // Stage s computes from buffer s&1, writes stage s+1 (held in `ready`) to
-    // buffer (s+1)&1 and loads stage s+2 into `prefetch` (past the end the
-    // offsets exceed the descriptor range: zeros, nothing read).
-    auto stage_body = [&](int s, v4u (&prefetch)[Q], const v4u (&ready)[Q]) {
-        const uint8_t *As = smem + (s & 1) * STAGE;
-        uint8_t *next = smem + ((s + 1) & 1) * STAGE;
+    // Stage s (the r-th of this range) computes from buffer r&1, writes stage
+    // s+1 (held in `ready`) to buffer (r+1)&1 and loads stage s+2 into
+    // `prefetch`.
+    auto stage_body = [&](int s, int r, v4u (&prefetch)[Q], const v4u (&ready)[Q]) {
+        const uint8_t *As = smem + (r & 1) * STAGE;
+        uint8_t *next = smem + ((r + 1) & 1) * STAGE;
         const int k2 = (s + 2) * BKT;
         auto kstep = [&](auto ksc) {
             constexpr int ks = decltype(ksc)::value;
@@ -566,18 +574,41 @@ __global__ __launch_bounds__(big::THREADS) void w8a8_gemm_stream_kernel(GemmArgs
         __syncthreads();
         read_frags(next, 0, 0);
     };
-    int s = 0;
-    for (; s + 1 < stages; s += 2) {
-        stage_body(s, regs0, regs1);
-        stage_body(s + 1, regs1, regs0);
+    const int n = s1 - s0;
+    int r = 0;
+    for (; r + 1 < n; r += 2) {
+        stage_body(s0 + r, r, regs0, regs1);
+        stage_body(s0 + r + 1, r + 1, regs1, regs0);
     }
-    if (s < stages) stage_body(s, regs0, regs1);
+    if (r < n) stage_body(s0 + r, r, regs0, regs1);
+}
 
+// Fused epilogue of a finished 256 x 256 tile (LDS free: callers synchronise first).
+template <int EPI>
+__device__ __forceinline__ void big_epilogue(const GemmArgs &args, uint8_t *smem, int m0, int n0,
+                                             const v16i (&acc)[big::TM][big::TN]) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = (wave & 3) >> 1;
+    const int wcol = (wave & 1) * 128 + (wave >> 2) * 64;
+    float *scales = reinterpret_cast<float *>(smem + 128 * 1024);
+    stage_scales<big::BM, big::BN, EPI>(args, scales, m0, n0);
+    store_tile_rows<EPI>(args, acc, m0, n0, wm, wcol, lane, smem, scales);
+}
+
+template <int EPI>
+__global__ __launch_bounds__(big::THREADS) void w8a8_gemm_stream_kernel(GemmArgs args) {
+    using namespace big;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE];
+    int ty, tx;
+    xcd_tile(blockIdx.x, (args.m + BM - 1) / BM, (args.n + BN - 1) / BN, 4, ty, tx);
+    const int m0 = ty * BM;
+    const int n0 = tx * BN;
+    v16i acc[TM][TN];
+    big_mainloop(args, smem, m0, n0, 0, args.k / BKT, acc);
     // Epilogue: LDS free once every wave is past its last fragment read.
     __syncthreads();
-    float *scales = reinterpret_cast<float *>(smem + 128 * 1024);
-    stage_scales<BM, BN, EPI>(args, scales, m0, n0);
-    store_tile_rows<EPI>(args, acc, m0, n0, wm, wcol, lane, smem, scales);
+    big_epilogue<EPI>(args, smem, m0, n0, acc);
 }
 
 // ----------------------------------------------------------------------------
@@ -879,6 +910,37 @@ int launch_stream(const GemmArgs &args, int epi, hipStream_t stream) {
     return launch("w8a8_gemm_stream_kernel", kernel, grid, dim3(big::THREADS), 0, stream, a2);
 }
 
+// Device address of a file-scope __device__ array on the current device,
+// looked up once per device with that device current (hipGetSymbolAddress):
+// host code passes this address to kernels, never the array's name.
+class DeviceSymbol {
+  public:
+    DeviceSymbol(const void *symbol, const char *what) : symbol_(symbol), what_(what) {}
+    int address(uint8_t **out) {
+        int device = -1;
+        if (hipGetDevice(&device) != hipSuccess || device < 0)
+            return fail(QXT_DEVICE_UNAVAILABLE, "%s: no current HIP device", what_);
+        std::lock_guard<std::mutex> guard(mutex_);
+        if (by_device_.size() <= static_cast<size_t>(device)) by_device_.resize(device + 1, nullptr);
+        if (by_device_[device] == nullptr) {
+            void *address = nullptr;
+            const hipError_t err = hipGetSymbolAddress(&address, symbol_);
+            if (err != hipSuccess || address == nullptr)
+                return fail(QXT_DEVICE_UNAVAILABLE, "%s: address on device %d: %s", what_, device,
+                            hipGetErrorString(err));
+            by_device_[device] = static_cast<uint8_t *>(address);
+        }
+        *out = by_device_[device];
+        return QXT_OK;
+    }
+
+  private:
+    const void *symbol_;
+    const char *what_;
+    std::mutex mutex_;
+    std::vector<uint8_t *> by_device_;
+};
+
 template <int MR, int RC, bool FUSED, int NT = kThreads>
 int launch_gemv_rc(GemmArgs args, const FusedRows &f, int epi, uint32_t layout, hipStream_t stream) {
     args.a_bytes = static_cast<uint32_t>(static_cast<size_t>(args.m - 1) * args.lda + args.k);
@@ -953,10 +1015,18 @@ int run_gemm(const GemmArgs &args, int epi, uint32_t layout, hipStream_t stream)
     const bool big = tm * tn >= cus;
     constexpr int D = QXT_GEMM_DEPTH, S = QXT_GEMM_STORE_KS;
     if (big && layout == QXT_W8A8_WEIGHT_NK && args.k % big::BKT == 0) {
-        // (Running the last, half-empty round of 16 x 56 tiles as a second
-        // launch of 256 x 128 tiles was measured at no gain on MI355X: the
-        // generic kernel needs as long for a half tile as this one for a
-        // full tile.)
+        // gate_up of cfg4 leaves its last round of 16 x 56 tiles half empty.
+        // Measured on MI355X, nothing that fills it was faster: a second
+        // launch of 256 x 128 tiles (the generic kernel needs as long for a
+        // half tile as this one for a full tile); a stream-K schedule over
+        // all tiles, bit-exact, 307-321 us against 240-248 us (the workgroups
+        // of an XCD no longer run in lockstep over shared A and B panels); the
+        // last round's tiles split in K over two workgroups, the partial sums
+        // passed through the output block: 300-320 us with device-scope
+        // release/acquire fences (each writes back the whole L2), equal to this
+        // kernel with write-through partial rows.  The board is power-bound:
+        // the same kernel reading constant operands instead of the matrices
+        // (a timing-only copy) runs gate_up in 199 us and down in 152 us.
         return launch_stream(args, epi, stream);
     }
     // Fewer 128 x 128 tiles than CUs (small M and N, e.g. one GPU's row shard
@@ -1022,27 +1092,13 @@ constexpr uint32_t kScratchMaxRows = kScratchScaleBytes / sizeof(float);
 
 static __device__ __align__(256) uint8_t scratch[kScratchRowBytes + kScratchScaleBytes];
 
-// Device address of `scratch`, looked up once per device with that device
-// current.  Host code never passes the array's name to a kernel or copy: on
-// the host that name is only a stand-in for the symbol, not a device address.
+// Device address of `scratch` on the current device (DeviceSymbol: looked up
+// once per device with that device current).  Host code never passes the
+// array's name to a kernel or copy: on the host that name is only a stand-in
+// for the symbol, not a device address.
 int scratch_address(uint8_t **out) {
-    static std::mutex mutex;
-    static std::vector<uint8_t *> by_device;
-    int device = -1;
-    if (hipGetDevice(&device) != hipSuccess || device < 0)
-        return fail(QXT_DEVICE_UNAVAILABLE, "w8a8 linear noalloc: no current HIP device");
-    std::lock_guard<std::mutex> guard(mutex);
-    if (by_device.size() <= static_cast<size_t>(device)) by_device.resize(device + 1, nullptr);
-    if (by_device[device] == nullptr) {
-        void *address = nullptr;
-        const hipError_t err = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
-        if (err != hipSuccess || address == nullptr)
-            return fail(QXT_DEVICE_UNAVAILABLE, "w8a8 linear noalloc: workspace address on device %d: %s", device,
-                        hipGetErrorString(err));
-        by_device[device] = static_cast<uint8_t *>(address);
-    }
-    *out = by_device[device];
-    return QXT_OK;
+    static DeviceSymbol symbol(HIP_SYMBOL(scratch), "w8a8 linear noalloc workspace");
+    return symbol.address(out);
 }
 
 }  // namespace

@@ -242,13 +242,15 @@ def test_whole_linear_bit_exact(m: int, k: int, n: int, seed: int) -> None:
     np.testing.assert_array_equal(y, oracle.w8a8_linear_reference(x, qw, sw, bias))
 
 
-@pytest.mark.parametrize("k,n", [(4096, 14336), (14336, 4096)], ids=["gate_up", "down"])
-def test_cfg4_shape_sampled_rows_bit_exact(k: int, n: int) -> None:
+@pytest.mark.parametrize("k,n,kernel", [(4096, 14336, "w8a8_gemm_stream_kernel"),
+                                        (14336, 4096, "w8a8_gemm_stream_kernel")], ids=["gate_up", "down"])
+def test_cfg4_shape_sampled_rows_bit_exact(k: int, n: int, kernel: str) -> None:
     # cfg4 (M=4096; gate_up K=4096, N=14336 and down K=14336, N=4096; seed 4;
     # 0.1% outlier channels x20): all rows on the GPU through the 256 x 256
-    # stream kernel (112 K stages at down), the oracle on 48 sampled rows (the
-    # oracle's cost, not the kernel's, sets the sample).  Mirrors the
-    # reference's assert_array_equal at tests/test_qpu_xla_gemm_int8.py:57-92.
+    # tiles (gate_up's 896 tiles in three and a half rounds, down's 256 with
+    # 112 K stages one per workgroup), the oracle on 48 sampled rows (the oracle's
+    # cost, not the kernel's, sets the sample).  Mirrors the reference's
+    # assert_array_equal at tests/test_qpu_xla_gemm_int8.py:57-92.
     from qpu_xla_amd import _lib
 
     rng = np.random.default_rng(4)
@@ -262,7 +264,7 @@ def test_cfg4_shape_sampled_rows_bit_exact(k: int, n: int) -> None:
     torch.cuda.synchronize()
     with _lib.launch_timing() as timing:
         y = w8a8_linear(xd, weight, bd)
-    assert "w8a8_gemm_stream_kernel" in [name for name, _ in timing.records]
+    assert kernel in [name for name, _ in timing.records]
     rows = np.sort(rng.choice(m, 48, replace=False))
     rows[0], rows[-1] = 0, m - 1
     qw, sw = oracle.quantize_per_output_channel_int8(w)
@@ -435,3 +437,47 @@ def test_fused_rows_at_register_chunk_boundaries_bit_exact(layout: str, m: int, 
         assert int(got_s[r : r + 1].view(np.uint32)[0]) == scale_bits
     expected = oracle.dequantize_epilogue(oracle.int8_gemm_i32(qa_ref, qw), sa_ref, sw, bias)
     np.testing.assert_array_equal(y.cpu().numpy(), expected)
+
+
+def _int8_case(seed: int, m: int, n: int, k: int):
+    rng = np.random.default_rng(seed)
+    a = rng.integers(-127, 128, size=(m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    sa = rng.uniform(0.001, 0.1, m).astype(np.float32)
+    sw = rng.uniform(0.001, 0.1, n).astype(np.float32)
+    bias = rng.standard_normal(n, dtype=np.float32)
+    return a, w, sa, sw, bias
+
+
+def test_large_tile_graph_replays_and_two_streams_bit_exact() -> None:
+    # The 256 x 256 stream kernel over 272 tiles (more than one round):
+    # launches on two streams at once, then one launch captured in a graph and
+    # replayed three times, every result checked in full.
+    m, n, k = 4096, 4352, 256
+    cases = [_int8_case(seed, m, n, k) for seed in (5, 6)]
+    wants = [oracle.dequantize_epilogue(oracle.int8_gemm_i32(a, w), sa, sw, bias) for a, w, sa, sw, bias in cases]
+    ops = [tuple(dev(t) for t in case) for case in cases]
+    outs = [torch.full((m, n), float("nan"), device="cuda") for _ in cases]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    for _ in range(2):  # concurrent eager launches
+        for (a, w, sa, sw, bias), out, stream in zip(ops, outs, streams):
+            with torch.cuda.stream(stream):
+                gemm_int8.w8a8_gemm_dequantize(a, w, sa, sw, bias, out=out, stream=stream)
+        torch.cuda.synchronize()
+        for out, want in zip(outs, wants):
+            np.testing.assert_array_equal(out.cpu().numpy(), want)
+            out.fill_(float("nan"))
+        torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    a, w, sa, sw, bias = ops[0]
+    capture = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=capture):
+        gemm_int8.w8a8_gemm_dequantize(a, w, sa, sw, bias, out=outs[0], stream=capture)
+    for _ in range(3):
+        outs[0].fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(outs[0].cpu().numpy(), wants[0])
