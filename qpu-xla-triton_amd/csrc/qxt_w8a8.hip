@@ -686,7 +686,12 @@ __device__ __forceinline__ void stage_rows(const GemmArgs &args, const FusedRows
         uint32_t *aw = reinterpret_cast<uint32_t *>(act);
         const int k4 = args.k / 4;
         for (int r = 0; r < MR; ++r) {
-            if (r >= args.m) {
+            // Row 0 always exists (every entry point requires m >= 1).  Its
+            // quantisation stays unconditional: behind an `r < m` branch the
+            // compiler sank the caller's early row loads into that branch,
+            // after the weight loads, and the row's first wait then waited for
+            // every weight load of the workgroup.
+            if (r > 0 && r >= args.m) {
                 for (int c = threadIdx.x; c < k4; c += NT) aw[r * k4 + c] = 0;
                 continue;
             }
@@ -710,25 +715,34 @@ __device__ __forceinline__ void stage_rows(const GemmArgs &args, const FusedRows
             amax = scratch[0];
 #pragma unroll
             for (int w = 1; w < NT / 64; ++w) amax = fmaxf(amax, scratch[w]);
-            __syncthreads();  // scratch is reused by the next row
+            if (r + 1 < MR) __syncthreads();  // scratch is reused by the next row
             const float sc = row_scale(amax, f.floor != 0);
-            // Through the scale's reciprocal, as rows_int8_kernel.
-            const bool recip = sc >= kRecipScaleMin;
-            const float rc = recip ? 1.0f / sc : 0.0f;
-            auto quant = [&](uint32_t bits) {
-                const float x = __uint_as_float(bits);
-                return recip ? quant_recip(x, sc, rc) : quant_div(x, sc);
-            };
+            // Through the scale's reciprocal, as rows_int8_kernel.  The choice
+            // is uniform over the workgroup: one branch around the row's loop,
+            // not one per element.
+            auto quantise_row = [&](auto recip_c) {
+                constexpr bool recip = decltype(recip_c)::value;
+                const float rc = recip ? 1.0f / sc : 0.0f;
+                auto quant = [&](uint32_t bits) {
+                    const float x = __uint_as_float(bits);
+                    return recip ? quant_recip(x, sc, rc) : quant_div(x, sc);
+                };
 #pragma unroll
-            for (int u = 0; u < RC; ++u) {
-                const int c = threadIdx.x + u * NT;
-                if (c >= k4) break;
-                const v4u v = xv[u];
-                const uint32_t word = pack_bytes(quant(v[0]), quant(v[1]), quant(v[2]), quant(v[3]));
-                aw[r * k4 + c] = word;
-                if (blockIdx.x == 0)
-                    reinterpret_cast<uint32_t *>(const_cast<int8_t *>(args.a) + static_cast<size_t>(r) * args.lda)[c] = word;
-            }
+                for (int u = 0; u < RC; ++u) {
+                    const int c = threadIdx.x + u * NT;
+                    if (c >= k4) break;
+                    const v4u v = xv[u];
+                    const uint32_t word = pack_bytes(quant(v[0]), quant(v[1]), quant(v[2]), quant(v[3]));
+                    aw[r * k4 + c] = word;
+                    if (blockIdx.x == 0)
+                        reinterpret_cast<uint32_t *>(const_cast<int8_t *>(args.a) + static_cast<size_t>(r) * args.lda)[c] =
+                            word;
+                }
+            };
+            if (sc >= kRecipScaleMin)
+                quantise_row(std::true_type{});
+            else
+                quantise_row(std::false_type{});
             if (threadIdx.x == 0) {
                 row_sa[r] = sc;
                 if (blockIdx.x == 0) const_cast<float *>(args.sa)[r] = sc;
@@ -738,7 +752,7 @@ __device__ __forceinline__ void stage_rows(const GemmArgs &args, const FusedRows
     __syncthreads();
 }
 
-// Weight [N, K] (K contiguous): each wave owns 4 output columns and streams
+// Weight [N, K] (K contiguous): each wave owns CPW output columns and streams
 // their K bytes 1 KB per load instruction (lane l takes bytes 16 l .. 16 l + 15
 // of each kilobyte), four kilobytes ahead of the one being reduced, the
 // first four requested before the activation is staged (after the first
@@ -746,11 +760,19 @@ __device__ __forceinline__ void stage_rows(const GemmArgs &args, const FusedRows
 // (measured on MI355X at the cfg4 shapes, M = 1: 17.1 -> 16.0 us for
 // K = 4096, N = 14336 and 18.2 -> 16.6 us for K = 14336, N = 4096; an
 // eight-kilobyte ring for long rows was no faster).  A wave sum per column
-// ends it.
+// ends it.  256-thread workgroups take 16 columns (4 per wave); the fused
+// 512-thread workgroups take 8, one per wave: twice the workgroups, so one
+// workgroup's row quantisation overlaps another's weight stream (cfg4 at
+// M = 1, rotated weights: 13.3 -> 12.9 us at K = 4096, N = 14336 and
+// 12.8 -> 11.8 us at K = 14336, N = 4096, event-timed medians).
 constexpr int kNonTemporal = 2;  // buffer-load cache policy bits: nt
-constexpr int kGemvColsNK = 16;  // per workgroup: 4 waves x 4 columns, or 8 waves x 2
+template <int NT>
+constexpr int gemv_cols_nk() {
+    return NT == 2 * kThreads ? 8 : 16;
+}
 template <int MR, int RC, int EPI, bool FUSED, int NT = kThreads>
 __global__ __launch_bounds__(NT) void w8a8_gemv_nk_kernel(GemmArgs args, FusedRows f) {
+    constexpr int kGemvColsNK = gemv_cols_nk<NT>();
     constexpr int CPW = kGemvColsNK / (NT / 64);  // columns per wave
     extern __shared__ v4u act[];  // [MR][K / 16]
     __shared__ float row_sa[4];
@@ -957,17 +979,19 @@ int launch_gemv_rc(GemmArgs args, const FusedRows &f, int epi, uint32_t layout, 
     auto kernel = epi == EPI_I32        ? w8a8_gemv_nk_kernel<MR, RC, EPI_I32, FUSED, NT>
                   : epi == EPI_DEQUANT ? w8a8_gemv_nk_kernel<MR, RC, EPI_DEQUANT, FUSED, NT>
                                        : w8a8_gemv_nk_kernel<MR, RC, EPI_DEQUANT_BIAS, FUSED, NT>;
-    return launch("w8a8_gemv_kernel", kernel, dim3((args.n + kGemvColsNK - 1) / kGemvColsNK), dim3(NT), lds, stream,
+    constexpr int cols = gemv_cols_nk<NT>();
+    return launch("w8a8_gemv_kernel", kernel, dim3((args.n + cols - 1) / cols), dim3(NT), lds, stream,
                   args, f);
 }
 
 // Fused rows are held as K / (4 * threads) chunks per thread, rounded up to
 // 4, 8 or 16 (fewer registers for short rows, more workgroups per CU).  The
-// [N, K] weights run 512-thread workgroups of eight waves with two columns
-// each: every thread then holds half as much of the row, so the workgroup's
+// [N, K] weights run 512-thread workgroups of eight waves (one column each):
+// every thread then holds half as much of the row, so the workgroup's
 // quantisation, which no weight can be reduced before, ends sooner
-// (measured on MI355X, cfg4 at M = 1 with rotated weights: down 16.4 ->
-// 14.9-15.1 us, gate_up 15.5-15.9 -> 15.2-15.3 us event-timed).
+// (measured on MI355X, cfg4 at M = 1 with rotated weights, two columns per
+// wave: down 16.4 -> 14.9-15.1 us, gate_up 15.5-15.9 -> 15.2-15.3 us
+// event-timed).
 #ifndef QXT_GEMV_WIDE
 #define QXT_GEMV_WIDE 1
 #endif

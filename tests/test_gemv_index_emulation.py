@@ -140,3 +140,26 @@ def test_k4n_waves_split_k_without_gap_or_overlap() -> None:
             for q in range(q0, q1):
                 hits[q] += 1
         assert np.all(hits == 1), k
+
+
+def gemv_cols_nk(nt: int) -> int:
+    """Output columns per [N, K] GEMV workgroup: 8 (one per wave) at 512 threads, else 16."""
+    return 8 if nt == 512 else 16
+
+
+@pytest.mark.parametrize("nt", [256, 512])
+def test_nk_columns_cover_every_output_once(nt: int) -> None:
+    # Workgroup b, wave w, slot j owns column b * cols + w * CPW + j; the grid
+    # has ceil(N / cols) workgroups and columns >= N read and write nothing.
+    cols = gemv_cols_nk(nt)
+    cpw = cols // (nt // 64)
+    assert cpw * (nt // 64) == cols and cpw >= 1
+    for n in (1, 7, 8, 16, 17, 256, 4096, 4100, 14336):
+        hits = np.zeros(n, np.int64)
+        for b in range(-(-n // cols)):
+            for w in range(nt // 64):
+                for j in range(cpw):
+                    c = b * cols + w * cpw + j
+                    if c < n:
+                        hits[c] += 1
+        assert np.all(hits == 1), (nt, n)
