@@ -219,6 +219,17 @@ __device__ __forceinline__ bool quantise_chunk(const float4 &v, int r, int rem, 
 // only after all of them.
 constexpr int kMaxPrefetchChunks = 6;
 
+// The prefetch value of one-row batches whose every activation is a native
+// Q8_0 row of at most kThreads blocks (K <= 8192, e.g. the Q8_0 written by a
+// pre-pass): each thread requests its block's 34 bytes before the weights
+// and the workgroup stages the row from registers, so the staging waits only
+// for the row.  (Requested after the weights, the staging of each workgroup
+// waited for all of its weight loads first, then fetched the row block by
+// block.)  Measured on MI355X, the cfg3 step's 7436-item batch: kernel
+// 81.5-82.6 -> 80.3-80.9 us, wall per step with the pre-pass 0.091 ->
+// 0.0865 ms (same box, alternating runs).
+constexpr int kQ8RowPrefetch = -1;
+
 // Chunks per thread that hold a one-row fp32 activation of `t` (2, 4 or 6),
 // or 0 when the task does not qualify.
 __host__ __device__ inline int prefetch_chunks(const Q4Task &t) {
@@ -327,11 +338,19 @@ __device__ __forceinline__ void stage_activation(const Q4Task &t, int r0, int *a
 // half-words each.  The loads are unconditional (indexes clamped into the
 // activation), so the compiler counts the weight loads issued after them
 // exactly and the staging waits only for these.
-template <int NT>
+template <int NT, int ITEMS = (512 + NT - 1) / NT>
 struct Q8RowRegs {
-    static constexpr int kItems = (512 + NT - 1) / NT;
+    static constexpr int kItems = ITEMS;
     uint32_t h[kItems][17];
 };
+
+// Keeps the compiler from moving memory accesses across this point.  Placed
+// after an activation row requested into registers ahead of the weights: the
+// row's later use sits behind a per-thread branch (threads past the row's
+// blocks have none), and without the barrier the compiler sinks the row's
+// loads into that branch, after the weight loads, so that the row's first
+// wait waits for every weight load.
+__device__ __forceinline__ void pin_memory_order() { asm volatile("" ::: "memory"); }
 
 template <int NT>
 __device__ __forceinline__ void fetch_q8_rows(const Q4Task &t, int r0, Q8RowRegs<NT> &a) {
@@ -380,10 +399,10 @@ __device__ __forceinline__ void stage_q8_rows(const Q4Task &t, const Q8RowRegs<N
 // blocks per thread, with unconditional loads (indexes clamped into the row)
 // like fetch_q8_rows; stage_q8_row writes its LDS image with the row-major
 // records.
-template <int NT>
-__device__ __forceinline__ void fetch_q8_row(const Q4Task &t, Q8RowRegs<NT> &a) {
+template <int NT, int ITEMS>
+__device__ __forceinline__ void fetch_q8_row(const Q4Task &t, Q8RowRegs<NT, ITEMS> &a) {
 #pragma unroll
-    for (int i = 0; i < Q8RowRegs<NT>::kItems; ++i) {
+    for (int i = 0; i < ITEMS; ++i) {
         const int b = min(static_cast<int>(threadIdx.x) + i * NT, t.blocks - 1);
         const QXT_GLOBAL uint16_t *p = global_in<uint16_t>(t.act + static_cast<size_t>(b) * Q8_0_BYTES);
 #pragma unroll
@@ -391,11 +410,11 @@ __device__ __forceinline__ void fetch_q8_row(const Q4Task &t, Q8RowRegs<NT> &a) 
     }
 }
 
-template <int NT>
-__device__ __forceinline__ void stage_q8_row(const Q4Task &t, const Q8RowRegs<NT> &a, int *aq, int *ad,
+template <int NT, int ITEMS>
+__device__ __forceinline__ void stage_q8_row(const Q4Task &t, const Q8RowRegs<NT, ITEMS> &a, int *aq, int *ad,
                                              const Q4Lds &geo) {
 #pragma unroll
-    for (int i = 0; i < Q8RowRegs<NT>::kItems; ++i) {
+    for (int i = 0; i < ITEMS; ++i) {
         const int b = static_cast<int>(threadIdx.x) + i * NT;
         if (b >= t.blocks) break;
         int words[8];
@@ -956,8 +975,10 @@ __device__ __forceinline__ void batch_item_split(const Q4Task &t, int col_base, 
     // quantised here) or a native Q8_0 row (PC == 0, blocks <= 512).
     float4 xv[PC > 0 ? PC : 1];
     Q8RowRegs<NT> a8;
+    // (Native rows are not pinned ahead of the weights here: pinned, cfg0's
+    // single linear measured 4.16 -> 4.55 us back to back on MI355X.)
     if constexpr (PC > 0) prefetch_row<PC, NT>(t, xv);
-    else fetch_q8_row<NT>(t, a8);
+    else fetch_q8_row(t, a8);
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int part = wave % S;
     const int u = (wave / S) * 64 + static_cast<int>(threadIdx.x & 63);
@@ -968,7 +989,7 @@ __device__ __forceinline__ void batch_item_split(const Q4Task &t, int col_base, 
     int *ad = aq + geo.aq_row;
     float *cb = reinterpret_cast<float *>(ad + geo.ad_row);
     if constexpr (PC > 0) quantise_row<PC, NT>(t, xv, aq, ad, geo);
-    else stage_q8_row<NT>(t, a8, aq, ad, geo);
+    else stage_q8_row(t, a8, aq, ad, geo);
     __syncthreads();
     if constexpr (S == 2) {
         if (part == 0) compute_part<2, 0>(G, units, u, pr, aq, ad, cb, geo);
@@ -993,14 +1014,20 @@ __device__ __forceinline__ void batch_item(const Q4Task &t, int col_base, int nc
     const int units = ncols * G;
     static_assert(PC == 0 || MR == 1, "the activation prefetch serves one-row batches");
     float4 xv[PC > 0 ? PC : 1];
+    Q8RowRegs<kThreads, 1> a8;
     if constexpr (PC > 0) prefetch_row<PC>(t, xv);
+    if constexpr (PC == kQ8RowPrefetch) {
+        fetch_q8_row(t, a8);
+        pin_memory_order();
+    }
     uint32_t wr[U][36];
-    load_units<U, LAYOUT, (PC > 0)>(t, col_base, G, units, 0, wr);
+    load_units<U, LAYOUT, (PC != 0)>(t, col_base, G, units, 0, wr);
     const Q4Lds geo(B, true);
     int *aq = lds;
     int *ad = aq + MR * geo.aq_row;
     float *cb = reinterpret_cast<float *>(ad + MR * geo.ad_row);
     if constexpr (PC > 0) quantise_row<PC>(t, xv, aq, ad, geo);
+    else if constexpr (PC == kQ8RowPrefetch) stage_q8_row(t, a8, aq, ad, geo);
     else stage_activation<MR>(t, 0, aq, ad, geo);
     __syncthreads();
     compute_fast<MR, U, false>(t, col_base, 0, G, units, 0, wr, aq, ad, cb, geo);
@@ -1311,6 +1338,11 @@ constexpr bool kSplitSingle = QXT_SPLIT_SINGLE != 0;
 #ifndef QXT_ARG_BATCH
 #define QXT_ARG_BATCH 1
 #endif
+
+#ifndef QXT_Q8_ROW_PREFETCH
+#define QXT_Q8_ROW_PREFETCH 1
+#endif
+constexpr bool kQ8RowPrefetchBatches = QXT_Q8_ROW_PREFETCH != 0;
 constexpr bool kArgBatches = QXT_ARG_BATCH != 0;
 
 static_assert(kPrefetchUnits >= 1 && kPrefetchUnits <= units_per_thread(1),
@@ -1485,7 +1517,7 @@ struct qxt_q4_0_batch {
     uint32_t grid = 0;
     int mr = 1;
     int layout = 0;  // WeightLayout of every task (kEitherLayout when mixed)
-    int prefetch = 0;  // activation chunks per thread prefetched (every task one fp32 row), or 0
+    int prefetch = 0;  // activation chunks per thread prefetched (every task one fp32 row), kQ8RowPrefetch, or 0
     int upt = 1;       // units per thread of the batch kernel
     int split = 1;     // waves per unit (one-row prefetch batches of narrow items)
     int threads = kThreads;  // 256, or 512 / 1024 for split prefetch batches
@@ -1544,6 +1576,7 @@ BatchKernel prefetch_kernel(int layout, int prefetch, int split, int threads) {
 BatchKernel batch_kernel(int mr, int layout, int prefetch, int upt, int split, int threads) {
     if (mr != 1) return batch_kernel_for<4, units_per_thread(4), 0>(layout);
     if (prefetch == 0) return batch_kernel_for<1, units_per_thread(1), 0>(layout);
+    if (prefetch == kQ8RowPrefetch) return batch_kernel_for<1, units_per_thread(1), kQ8RowPrefetch>(layout);
     return upt == 1 ? prefetch_kernel<1>(layout, prefetch, split, threads)
                     : prefetch_kernel<units_per_thread(1)>(layout, prefetch, split, threads);
 }
@@ -1887,6 +1920,14 @@ int qxt_q4_0_batch_prepare(const qxt_q4_0_task *tasks, uint32_t count, qxt_q4_0_
     batch->upt = upt;
     if (prefetch_candidate)
         for (const Q4Task &t : host) batch->prefetch = std::max(batch->prefetch, prefetch_chunks(t));
+    if (kQ8RowPrefetchBatches && mr == 1 && batch->prefetch == 0 && upt == units_per_thread(1)) {
+        // Every activation a native Q8_0 row (given, or written by the
+        // pre-pass) of at most one block per thread: its blocks are requested
+        // before the weights.
+        bool q8_rows = true;
+        for (const Q4Task &t : host) q8_rows = q8_rows && t.x == nullptr && t.rows == 1 && t.blocks <= kThreads;
+        if (q8_rows) batch->prefetch = kQ8RowPrefetch;
+    }
     if (prefetch_candidate && upt == 1 && kSplitUnits) {
         // Items of at most 64 (128) units: each unit split over 4 (2) waves.
         // Measured on MI355X, the staged decode of cfg3 (q/k/v items of 88

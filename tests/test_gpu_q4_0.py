@@ -635,6 +635,43 @@ def test_one_row_fp32_stage_batches_with_activation_prefetch_bit_exact(shapes) -
                 _check_batch(batch_tasks, expected)
 
 
+@pytest.mark.parametrize("k_last", [8192, 8448])
+def test_prepass_batch_native_row_prefetch_bit_exact(k_last: int) -> None:
+    # A batch of more than 1024 work items runs the Q8_0 pre-pass; when every
+    # resulting row has at most 256 blocks (K <= 8192) each workgroup requests
+    # its row's blocks before its weights, otherwise (one task at K = 8448)
+    # the whole batch stages rows after the weights.  Both bit-exact, with a
+    # caller-given native Q8_0 row among the pre-pass rows.
+    rng = np.random.default_rng(4096 + k_last)
+    shared = {}
+    tasks, expected = [], []
+    shapes = [(8192, 2048)] * 7 + [(k_last, 2048), (2048, 256)]
+    for i, (k, n) in enumerate(shapes):
+        if k not in shared:
+            w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+            shared[k] = oracle.quantize_q4_0_blocks(w)
+        wq = shared[k][:n]
+        x = rng.standard_normal((1, k), dtype=np.float32)
+        x[0, 32:64] = 0.0
+        xq = oracle.quantize_q8_0_blocks(x)
+        task = {"weight": dev(wq), "destination": torch.full((1, n + 16), float(SENTINEL), device="cuda"),
+                "weight_column_start": 0, "output_column_start": 16, "column_count": n}
+        if i == 3:
+            task["activation"] = dev(xq)
+        else:
+            task["x"] = dev(x)
+        tasks.append(task)
+        expected.append(oracle.q4_0_q8_0_reference(xq, wq))
+    with q4.Q4_0LinearBatch(tasks) as batch:
+        assert batch.work_items > 1024
+        for _ in range(2):
+            for t in tasks:
+                t["destination"][:, 16:] = -1.0
+            batch.launch()
+            torch.cuda.synchronize()
+            _check_batch(tasks, expected)
+
+
 def test_batch_prepare_allocations_are_counted() -> None:
     # The library counts its own device allocations (qxt_allocation_count):
     # preparing a batch allocates its device tables, launching it does not.
