@@ -672,6 +672,32 @@ def test_prepass_batch_native_row_prefetch_bit_exact(k_last: int) -> None:
             _check_batch(tasks, expected)
 
 
+@pytest.mark.parametrize("count", [1, 4, 5])
+@pytest.mark.parametrize("k_big", [8192, 8448])
+def test_native_row_batches_in_arguments_and_tables_bit_exact(count: int, k_big: int) -> None:
+    # Every task hands over a native Q8_0 row: batches of at most 256 blocks
+    # per row request each row before the weights (up to four tasks in the
+    # kernel arguments, more in device tables); a task of 264 blocks (K =
+    # 8448) makes the whole batch stage rows after the weights.  Ragged
+    # tiles end every task; a second launch repeats the result.
+    shapes = [(1, k_big, 300, 0, 300), (1, 2048, 700, 4, 690), (1, 256, 64, 0, 64), (1, 4096, 96, 16, 77),
+              (1, 5632, 130, 0, 130)][:count]
+    tasks, expected = _batch_case(700 + count + k_big, shapes, fused_every=len(shapes) + 1)
+    assert all("activation" in t for t in tasks[1:]) and "x" in tasks[0]
+    # Task 0 too: give it its Q8_0 row instead of the fp32 row.
+    x0 = tasks[0].pop("x").cpu().numpy()
+    tasks[0]["activation"] = dev(oracle.quantize_q8_0_blocks(x0))
+    stream = torch.cuda.Stream()
+    with q4.Q4_0LinearBatch(tasks) as batch:
+        assert batch.task_count == count
+        for _ in range(2):
+            for t in tasks:
+                t["destination"][:, 16:] = -1.0
+            batch.launch(stream)
+            stream.synchronize()
+            _check_batch(tasks, expected)
+
+
 def test_batch_prepare_allocations_are_counted() -> None:
     # The library counts its own device allocations (qxt_allocation_count):
     # preparing a batch allocates its device tables, launching it does not.
