@@ -19,6 +19,8 @@
 #include <cmath>
 #include <cstring>
 
+#include <type_traits>
+
 #include "qxt_common.h"
 
 namespace qxt {
@@ -293,21 +295,29 @@ __global__ __launch_bounds__(kThreads) void rows_int8_kernel(const float *__rest
     // Every row scale of the 1/127 floor takes the reciprocal form (measured
     // on MI355X at 4096 rows: K = 14336 50.8 -> 47.0 us, K = 4096 15.6 ->
     // 14.4 us against a division per element).
-    const bool recip = s >= kRecipScaleMin;
-    const float r = recip ? 1.0f / s : 0.0f;
-    auto quant = [&](float x) { return recip ? quant_recip(x, s, r) : quant_div(x, s); };
+    // The choice is uniform over the workgroup: one branch around the row's
+    // loop, not one per element.
+    auto quantise = [&](auto recip_c) {
+        constexpr bool recip = decltype(recip_c)::value;
+        const float r = recip ? 1.0f / s : 0.0f;
+        auto quant = [&](float x) { return recip ? quant_recip(x, s, r) : quant_div(x, s); };
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const uint32_t c = threadIdx.x + i * kThreads;
-        if (c < chunks) {
-            const uint32_t word = pack_bytes(quant(v[i].x), quant(v[i].y), quant(v[i].z), quant(v[i].w));
-            if constexpr (VEC) {
-                *reinterpret_cast<uint32_t *>(dst + 4 * c) = word;
-            } else {
-                for (int j = 0; j < 4; ++j) dst[4 * c + j] = static_cast<int8_t>((word >> (8 * j)) & 0xFF);
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t c = threadIdx.x + i * kThreads;
+            if (c < chunks) {
+                const uint32_t word = pack_bytes(quant(v[i].x), quant(v[i].y), quant(v[i].z), quant(v[i].w));
+                if constexpr (VEC) {
+                    *reinterpret_cast<uint32_t *>(dst + 4 * c) = word;
+                } else {
+                    for (int j = 0; j < 4; ++j) dst[4 * c + j] = static_cast<int8_t>((word >> (8 * j)) & 0xFF);
+                }
             }
         }
-    }
+    };
+    if (s >= kRecipScaleMin)
+        quantise(std::true_type{});
+    else
+        quantise(std::false_type{});
     for (uint32_t c = columns + threadIdx.x; c < padded; c += kThreads) dst[c] = 0;
     if (threadIdx.x == 0) scales[row] = s;
 }
