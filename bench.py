@@ -682,7 +682,9 @@ def leg_w8a8_gemv(torch, args) -> dict:
                        _p(wt.scales), _p(bias), _p(y), _rs(y), 1, n, k, 0, 0, runner.handle)
         runner.run()
         torch.cuda.synchronize()
-        times = runner.kernel_times(repeats=2)
+        # Five passes over the copies (50 event-timed launches): a single
+        # launch's device time varies by several percent from launch to launch.
+        times = runner.kernel_times(repeats=5)
         gemv_us = float(np.mean(times["w8a8_gemv_kernel"])) * 1e3
         graph = runner.capture()
         wall_ms, _ = runner.timed_graph(graph, max(2, args.steps // 4), 2)
@@ -695,7 +697,7 @@ def leg_w8a8_gemv(torch, args) -> dict:
             "gemv_frac_hbm": b / (gemv_us * 1e-6) / 1e9 / PEAK_HBM_GBS,
             "operator_us": wall_ms * 1e3 / copies,
             # M <= 4 quantises inside the GEMV kernel: one launch per operator call.
-            "launches_per_call": sum(len(v) for v in times.values()) // (2 * copies),
+            "launches_per_call": sum(len(v) for v in times.values()) // (5 * copies),
         }
         torch.cuda.synchronize()
         checked = sorted({0, copies // 2, copies - 1})
