@@ -82,6 +82,33 @@ def test_gemm_i32_random_shapes_exact(m: int, n: int, k: int) -> None:
     np.testing.assert_array_equal(out.cpu().numpy(), oracle.int8_gemm_i32(a, w))
 
 
+def test_mid_size_tiles_both_layouts_and_epilogue_exact() -> None:
+    # Fewer 256 x 256 tiles than CUs but at least as many 128 x 128 ones: the
+    # 128 x 128 kernel, over [N, K] weights with ragged M, N and a K that is
+    # not a multiple of its 64-byte stage (int32 and fused epilogue), and over
+    # the packed-K4 [K/4, N] words of the reference's tiled contract.
+    rng = np.random.default_rng(1280)
+    m, n, k = 520, 8200, 208
+    a = rng.integers(-127, 128, size=(m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    want = oracle.int8_gemm_i32(a, w)
+    np.testing.assert_array_equal(gemm_int8.w8a8_gemm_i32(dev(a), dev(w)).cpu().numpy(), want)
+    sa = rng.uniform(0.001, 0.1, m).astype(np.float32)
+    sw = rng.uniform(0.001, 0.1, n).astype(np.float32)
+    bias = rng.standard_normal(n, dtype=np.float32)
+    out = gemm_int8.w8a8_gemm_dequantize(dev(a), dev(w), dev(sa), dev(sw), dev(bias)).cpu().numpy()
+    np.testing.assert_array_equal(out, oracle.dequantize_epilogue(want, sa, sw, bias))
+    p_, q_, r_ = 512, 208, 8192
+    left_v = rng.integers(-127, 128, size=(p_, q_), dtype=np.int8)
+    right_v = rng.integers(-127, 128, size=(q_, r_), dtype=np.int8)
+    left, right = oracle.pack_int8_gemm_operands(left_v, right_v)
+    destination = torch.empty((p_, r_), dtype=torch.int32, device="cuda")
+    with Queue() as queue:
+        queue.submit(gemm_int8.TILED_W8A8_GEMM_KERNEL, (words(left), words(right), destination),
+                     grid=(r_ // 16, p_ // 16, 1)).wait()
+    np.testing.assert_array_equal(destination.cpu().numpy(), (left_v.astype(np.int64) @ right_v.astype(np.int64)).astype(np.int32))
+
+
 def test_streaming_kernel_fused_epilogue_on_edge_tiles_bit_exact() -> None:
     rng = np.random.default_rng(2718)
     m, n, k = 4000, 4100, 512
