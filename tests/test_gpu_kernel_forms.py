@@ -119,3 +119,54 @@ def test_native_prefill_on_a_large_grid_sampled_rows() -> None:
     y = ggml_q4_0_q8_0_linear(dev(xq), dev(wq)).cpu().numpy()
     rows = np.array([0, 1, 63, 64, 255, 448, m - 1])
     np.testing.assert_array_equal(y[rows], oracle.q4_0_q8_0_reference(xq[rows], wq))
+
+
+@pytest.mark.parametrize("with_bias", [True, False])
+@pytest.mark.parametrize("m,k", [(1, 16), (2, 1040), (4, 4096)])
+def test_packed_k4_fused_linear_short_rows(m: int, k: int, with_bias: bool) -> None:
+    # qxt_w8a8_linear over packed-K4 [K/4, N] weights at K <= 4096: the
+    # 256-thread K4N GEMV holding each fp32 row as four 16-byte chunks per
+    # thread, quantising it inside every workgroup.
+    from qpu_xla_amd import _lib
+    from qpu_xla_amd._tensors import ptr, row_stride
+
+    rng = np.random.default_rng(900 + m + k + with_bias)
+    n = 132
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    wf = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    qw, sw = oracle.quantize_per_output_channel_int8(wf)
+    bias = (rng.standard_normal(n, dtype=np.float32) * np.float32(0.1)).astype(np.float32)
+    w_d = words(np.ascontiguousarray(oracle.pack_int8_quads(qw).T))
+    xd, sw_d, b_d = dev(x), dev(sw), dev(bias)
+    qa = torch.empty((m, k), dtype=torch.int8, device="cuda")
+    sa = torch.empty((m,), dtype=torch.float32, device="cuda")
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    _lib.call("qxt_w8a8_linear", ptr(xd), row_stride(xd), ptr(qa), row_stride(qa), ptr(sa), ptr(w_d), row_stride(w_d),
+              ptr(sw_d), ptr(b_d) if with_bias else None, ptr(y), row_stride(y), m, n, k, _lib.WEIGHT_K4N, 0, None)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(y.cpu().numpy(), oracle.w8a8_linear_reference(x, qw, sw, bias if with_bias else None))
+
+
+@pytest.mark.parametrize("m", [1, 2, 4])
+def test_gemv_epilogue_without_bias_both_layouts(m: int) -> None:
+    # Stored int8 rows (M <= 4): the GEMV kernels' dequantising epilogue
+    # without the bias add, over [N, K] and packed-K4 weights.
+    from qpu_xla_amd import _lib
+    from qpu_xla_amd._tensors import ptr, row_stride
+
+    rng = np.random.default_rng(40 + m)
+    n, k = 4096, 2048
+    a = rng.integers(-127, 128, size=(m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    sa = rng.uniform(0.001, 0.1, m).astype(np.float32)
+    sw = rng.uniform(0.001, 0.1, n).astype(np.float32)
+    expected = oracle.dequantize_epilogue(oracle.int8_gemm_i32(a, w), sa, sw)
+    y = gemm_int8.w8a8_gemm_dequantize(dev(a), dev(w), dev(sa), dev(sw)).cpu().numpy()
+    np.testing.assert_array_equal(y, expected)
+    left, right = oracle.pack_int8_gemm_operands(a, np.ascontiguousarray(w.T))
+    lw, rw, sa_d, sw_d = words(left), words(right), dev(sa), dev(sw)
+    out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    _lib.call("qxt_w8a8_gemm_dequantize", ptr(lw), row_stride(lw), ptr(rw), row_stride(rw), ptr(sa_d), ptr(sw_d),
+              None, ptr(out), row_stride(out), m, n, k, _lib.WEIGHT_K4N, None)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), expected)
