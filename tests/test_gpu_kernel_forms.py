@@ -170,3 +170,49 @@ def test_gemv_epilogue_without_bias_both_layouts(m: int) -> None:
               None, ptr(out), row_stride(out), m, n, k, _lib.WEIGHT_K4N, None)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(out.cpu().numpy(), expected)
+
+
+SENTINEL = np.float32(123456.0)
+
+
+@pytest.mark.parametrize("rows,k,n,layout", [
+    (1, 4096, 8192, "native"),   # 16 columns x 16 units = 256 units per tile: split units over two waves
+    (1, 4096, 8192, "lanes"),
+    (1, 2048, 16384, "lanes"),   # 32 columns x 8 units, the same split form
+    (1, 4096, 16384, "lanes"),   # 512 units per tile: the two-units-per-thread lane kernel
+    (3, 2048, 700, "lanes"),     # three rows over lane weights
+    (2, 288, 100, "native"),     # 9 blocks per row (not a multiple of 8): the general kernel
+    (3, 288, 70, "native"),
+])
+def test_q4_0_single_linear_forms_bit_exact(rows: int, k: int, n: int, layout: str) -> None:
+    from qpu_xla_amd.kernels import ggml_q4_0 as q4
+
+    rng = np.random.default_rng(rows * 100000 + k + n)
+    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    x = rng.standard_normal((rows, k), dtype=np.float32)
+    wq, xq = oracle.quantize_q4_0_blocks(w), oracle.quantize_q8_0_blocks(x)
+    ncols = n - 4
+    out = torch.full((rows, ncols + 16), float(SENTINEL), device="cuda")
+    if layout == "lanes":
+        q4.ggml_q4_0_q8_0_lane_linear(dev(xq), q4.pack_ggml_q4_0_lane_weights(dev(wq)), out, weight_column_start=4,
+                                      output_column_start=16, column_count=ncols)
+    else:
+        q4.ggml_q4_0_q8_0_linear(dev(xq), dev(wq), out, weight_column_start=4, output_column_start=16,
+                                 column_count=ncols)
+    got = out.cpu().numpy()
+    np.testing.assert_array_equal(got[:, :16], SENTINEL)
+    np.testing.assert_array_equal(got[:, 16:], oracle.q4_0_q8_0_reference(xq, wq[4:]))
+
+
+@pytest.mark.parametrize("rows", [2, 3])
+def test_q4_0_block_dots_general_kernel(rows: int) -> None:
+    # The debug block-dot path on rows whose blocks are not a multiple of 8.
+    from qpu_xla_amd.kernels import ggml_q4_0 as q4
+
+    rng = np.random.default_rng(77 + rows)
+    k, n = 288, 48
+    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    x = rng.standard_normal((rows, k), dtype=np.float32)
+    wq, xq = oracle.quantize_q4_0_blocks(w), oracle.quantize_q8_0_blocks(x)
+    dots = q4.ggml_q4_0_q8_0_block_dots(dev(xq), dev(wq)).cpu().numpy()
+    np.testing.assert_array_equal(dots, oracle.q4_0_q8_0_block_dots(xq, wq))
