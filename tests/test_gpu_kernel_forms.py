@@ -216,3 +216,75 @@ def test_q4_0_block_dots_general_kernel(rows: int) -> None:
     wq, xq = oracle.quantize_q4_0_blocks(w), oracle.quantize_q8_0_blocks(x)
     dots = q4.ggml_q4_0_q8_0_block_dots(dev(xq), dev(wq)).cpu().numpy()
     np.testing.assert_array_equal(dots, oracle.q4_0_q8_0_block_dots(xq, wq))
+
+
+_STAGE_WEIGHTS: dict = {}
+
+
+def _stage_weight(k: int):
+    """One quantised [6144, K] weight per K, shared by the stage-batch cases (oracle quantisation is slow)."""
+    if k not in _STAGE_WEIGHTS:
+        rng = np.random.default_rng(8000 + k)
+        w = (rng.standard_normal((6144, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+        _STAGE_WEIGHTS[k] = oracle.quantize_q4_0_blocks(w)
+    return _STAGE_WEIGHTS[k]
+
+
+@pytest.mark.parametrize("layout", ["native", "lanes", "mixed"])
+@pytest.mark.parametrize("count", [1, 5])
+@pytest.mark.parametrize("n", [1024, 6144])
+@pytest.mark.parametrize("k", [2048, 4096, 6144])
+def test_fp32_row_stage_batches_every_prefetch_form(k: int, n: int, count: int, layout: str) -> None:
+    # One-row batches of fp32 activations (quantised inside each workgroup,
+    # the row requested before the weights as 2, 4 or 6 chunks per thread of
+    # 256, i.e. 1, 2 or 3 of 512), tiles narrowed until they fill the chip and
+    # each unit split over four or two waves, tasks in the kernel arguments
+    # (one) or in device tables (five), over native, lane or mixed weights.
+    from qpu_xla_amd.kernels import ggml_q4_0 as q4
+
+    wq_all = _stage_weight(k)
+    rng = np.random.default_rng(k + n + count)
+    tasks, expected = [], []
+    for i in range(count):
+        ncols = n // count - 4 * i
+        wcol0 = 8 * i
+        wq = wq_all[wcol0:wcol0 + ncols]
+        x = rng.standard_normal((1, k), dtype=np.float32)
+        weight = dev(wq_all)
+        if layout == "lanes" or (layout == "mixed" and i % 2 == 0):
+            weight = q4.pack_ggml_q4_0_lane_weights(weight)
+        tasks.append({"weight": weight, "x": dev(x), "weight_column_start": wcol0, "output_column_start": 16,
+                      "column_count": ncols,
+                      "destination": torch.full((1, ncols + 16), float(SENTINEL), device="cuda")})
+        expected.append(oracle.q4_0_q8_0_reference(oracle.quantize_q8_0_blocks(x), wq))
+    with q4.Q4_0LinearBatch(tasks) as batch:
+        batch.launch()
+        torch.cuda.synchronize()
+    for t, want in zip(tasks, expected):
+        got = t["destination"].cpu().numpy()
+        np.testing.assert_array_equal(got[:, :16], SENTINEL)
+        np.testing.assert_array_equal(got[:, 16:], want)
+
+
+@pytest.mark.parametrize("layout", ["native", "lanes"])
+@pytest.mark.parametrize("k,n", [(2048, 20480), (4096, 9216), (6144, 6144)])
+def test_fp32_row_batch_of_full_width_tiles(k: int, n: int, layout: str) -> None:
+    # Enough columns for one full-width tile per CU (256 to 1024 work items):
+    # two units per thread, the fp32 row still requested before the weights.
+    from qpu_xla_amd.kernels import ggml_q4_0 as q4
+
+    rng = np.random.default_rng(k * 3 + n)
+    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    wq = oracle.quantize_q4_0_blocks(w)
+    x = rng.standard_normal((1, k), dtype=np.float32)
+    weight = dev(wq)
+    if layout == "lanes":
+        weight = q4.pack_ggml_q4_0_lane_weights(weight)
+    task = {"weight": weight, "x": dev(x), "weight_column_start": 0, "output_column_start": 0, "column_count": n,
+            "destination": torch.full((1, n), float(SENTINEL), device="cuda")}
+    with q4.Q4_0LinearBatch([task]) as batch:
+        assert 256 <= batch.work_items <= 1024
+        batch.launch()
+        torch.cuda.synchronize()
+    np.testing.assert_array_equal(task["destination"].cpu().numpy(),
+                                  oracle.q4_0_q8_0_reference(oracle.quantize_q8_0_blocks(x), wq))
