@@ -288,3 +288,79 @@ def test_fp32_row_batch_of_full_width_tiles(k: int, n: int, layout: str) -> None
         torch.cuda.synchronize()
     np.testing.assert_array_equal(task["destination"].cpu().numpy(),
                                   oracle.q4_0_q8_0_reference(oracle.quantize_q8_0_blocks(x), wq))
+
+
+def _q8_operands(seed: int, rows: int, outputs: int, blocks: int):
+    rng = np.random.default_rng(seed)
+    act = oracle.pack_q8_0_blocks(rng.uniform(-0.1, 0.1, (rows, blocks)).astype(np.float16),
+                                  rng.integers(-128, 128, (rows, blocks, 32)))
+    wt = oracle.pack_q8_0_blocks(rng.uniform(-0.1, 0.1, (outputs, blocks)).astype(np.float16),
+                                 rng.integers(-128, 128, (outputs, blocks, 32)))
+    return act, wt
+
+
+@pytest.mark.parametrize("rows,blocks,weight_offset", [
+    (1, 3, 0),    # one row, blocks % 8 != 0: one block per thread
+    (2, 5, 0),    # two rows, one block per thread
+    (3, 16, 0),   # three rows, eight blocks per thread (16-byte aligned weight rows)
+    (2, 8, 2),    # weights 2 bytes past a 16-byte boundary: one block per thread
+])
+def test_q8_0_linear_row_counts_and_weight_alignment(rows: int, blocks: int, weight_offset: int) -> None:
+    # The Q8_0 x Q8_0 linear at one, two and three rows per workgroup, with
+    # and without the eight-blocks-per-thread weight reads (those need
+    # blocks % 8 == 0 and 16-byte aligned weight rows).
+    from qpu_xla_amd.kernels import ggml_q8_0 as q8
+
+    act, wt = _q8_operands(5300 + rows * 10 + blocks, rows, 96, blocks)
+    storage = torch.zeros(wt.size + weight_offset, dtype=torch.uint8, device="cuda")
+    weight = storage[weight_offset:].view(wt.shape)
+    weight.copy_(torch.from_numpy(wt))
+    assert weight.is_contiguous() and (weight.data_ptr() % 16 != 0) == (weight_offset != 0)
+    out = torch.full((rows, 80 + 16), float(SENTINEL), device="cuda")
+    q8.ggml_q8_0_q8_0_linear(dev(act), weight, out, weight_column_start=7, output_column_start=16, column_count=80)
+    got = out.cpu().numpy()
+    np.testing.assert_array_equal(got[:, :16], SENTINEL)
+    np.testing.assert_array_equal(got[:, 16:], oracle.q8_0_q8_0_reference(act, wt[7:87]))
+
+
+def _offset_rows(values: np.ndarray) -> torch.Tensor:
+    # A view whose rows start 4 bytes into an allocation with one spare
+    # column: neither the base pointer nor the row stride is 16-byte aligned.
+    rows, columns = values.shape
+    base = torch.zeros((rows, columns + 1), dtype=torch.float32, device="cuda")
+    view = base[:, 1:]
+    view.copy_(torch.from_numpy(values))
+    assert view.data_ptr() % 16 != 0 and (view.stride(0) * 4) % 16 != 0
+    return view
+
+
+@pytest.mark.parametrize("rows,columns", [(3, 96), (17, 2048)])
+def test_quantisers_on_unaligned_rows_bit_exact(rows: int, columns: int) -> None:
+    # The scalar-load forms of the Q8_0 and Q4_0 quantisers.
+    from qpu_xla_amd.kernels.quantize import quantize_q4_0, quantize_q8_0
+
+    rng = np.random.default_rng(rows + columns)
+    x = rng.standard_normal((rows, columns), dtype=np.float32)
+    x[0, :32] = 0.0  # an all-zero block
+    np.testing.assert_array_equal(quantize_q8_0(_offset_rows(x)).cpu().numpy(), oracle.quantize_q8_0_blocks(x))
+    np.testing.assert_array_equal(quantize_q4_0(_offset_rows(x)).cpu().numpy(), oracle.quantize_q4_0_blocks(x))
+
+
+@pytest.mark.parametrize("rows,columns", [(5, 160), (64, 33 * 1024)])  # gather kernel; >= 65536 blocks: LDS band
+def test_geglu_on_unaligned_rows_every_output_layout(rows: int, columns: int) -> None:
+    # The scalar-load forms of both GEGLU kernels, writing native blocks and
+    # split planes with four- and two-byte scales.
+    from qpu_xla_amd.kernels import ggml_geglu_q8 as geglu
+
+    rng = np.random.default_rng(rows * 7 + columns)
+    gate = rng.normal(0.0, 1.5, (rows, columns)).astype(np.float32)
+    up = rng.normal(0.0, 1.0, (rows, columns)).astype(np.float32)
+    gate_d, up_d = _offset_rows(gate), _offset_rows(up)
+    np.testing.assert_array_equal(geglu.ggml_geglu_q8_0(gate_d, up_d).cpu().numpy(),
+                                  oracle.geglu_q8_0_reference(gate, up))
+    words, planes = oracle.geglu_q8_0_split_reference(gate, up)
+    for dtype, view in ((torch.int32, np.uint32), (torch.int16, np.uint16)):
+        scales = torch.empty((rows, columns // 32), dtype=dtype, device="cuda")
+        scales, values = geglu.ggml_geglu_q8_0_split(gate_d, up_d, scales=scales)
+        np.testing.assert_array_equal(scales.cpu().numpy().view(view).astype(np.uint32), words)
+        np.testing.assert_array_equal(values.cpu().numpy(), planes)
