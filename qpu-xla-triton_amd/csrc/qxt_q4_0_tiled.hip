@@ -605,6 +605,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, SEL
                     }
                 }
             }
+            if constexpr (!SELECT) {
+                // One wave per SIMD: issue each block's MFMA ahead of the
+                // previous block's scaling (measured on MI355X at M = 512,
+                // K = 5632, N = 2048: 46.7 -> 44.8 us; the large-grid form,
+                // whose other workgroups cover the latency, got slower).
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (half + j + 1 < kGroup) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 48, 0);  // VALU: one block's scaling
+                }
+            }
         }
         // The other buffer was last read a group ago (before the previous
         // barrier): fill it with the next group and load the one after.
