@@ -16,9 +16,11 @@ Also reported on the same JSON line:
                           operator and GEMM-only, with an int8-MFMA roofline;
   * ``configs``       -- cfg0 (rotated over >= 512 MB of weight copies), cfg1, cfg2 (lane layout,
                          and over the native ggml rows);
+  * ``q8_0_q8_0``     -- the Q8_0 x Q8_0 linear (native blocks) at M = 1 and M = 4 decode
+                         shapes, rotated weights, in GB/s against the HBM peak;
   * ``cpu_baseline``  -- the NumPy oracle of the reference CPU path on this host.
 
-Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--legs decode,w8a8,gemv,prefill,geglu,shards,cfg0,cfg1,cfg2,copy,cpu]
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--legs decode,w8a8,gemv,prefill,geglu,q8_0,shards,cfg0,cfg1,cfg2,copy,cpu]
 Weights and activations are synthetic (seeded random, the BASELINE distributions).
 """
 
@@ -69,7 +71,7 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--legs", default="decode,w8a8,gemv,prefill,geglu,shards,cfg0,cfg1,cfg2,copy,cpu")
+    ap.add_argument("--legs", default="decode,w8a8,gemv,prefill,geglu,q8_0,shards,cfg0,cfg1,cfg2,copy,cpu")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of each CPU-baseline sample")
     return ap.parse_args()
 
@@ -544,6 +546,78 @@ def leg_rotated_q4(torch, args, rows: int, k: int, n: int, seed: int, layout: st
     torch.cuda.synchronize()
     out["check"] = check_q4_0(torch, out["shape"], q8_0_host(torch, x), last_native, y, rows=tuple(range(rows)))
     del graph, weights, last_native
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
+def q8_linear_bytes(m: int, k: int, n: int) -> int:
+    """Algorithmic bytes of one Q8_0 x Q8_0 linear: weights + Q8_0 activation + fp32 output."""
+    return n * (k // 32) * 34 + m * (k // 32) * 34 + m * n * 4
+
+
+def check_q8_0_q8_0(torch, label: str, act_blocks, w_blocks, output, rows=(0,)) -> dict:
+    """output[r, :N] == sum_b fl32(fl32(float(dot_b) * da) * dw) in block order (activation scale first)."""
+    w = w_blocks.cpu()
+    dw = _fp16_field(torch, w)  # [N, B]
+    qw = w[..., 2:].view(torch.int8).to(torch.int32)  # [N, B, 32]
+    for r in rows:
+        a = act_blocks[r].cpu()
+        da = _fp16_field(torch, a)  # [B]
+        qa = a[..., 2:].view(torch.int8).to(torch.int32)  # [B, 32]
+        dots = (qw * qa).sum(-1)  # [N, B], exact
+        acc = torch.zeros(w.shape[0], dtype=torch.float32)
+        for b in range(w.shape[1]):
+            acc = acc + (dots[:, b].float() * da[b]) * dw[:, b]
+        got = output[r, : w.shape[0]].cpu()
+        if not torch.equal(got, acc):
+            raise _mismatch(torch, label, r, got, acc, {"weight scales": dw, "activation scales": da})
+    return {"rows_checked": list(rows), "columns": int(w.shape[0]), "bit_exact": True}
+
+
+def leg_rotated_q8(torch, args, rows: int, k: int, n: int, seed: int) -> dict:
+    """One Q8_0 x Q8_0 linear shape (native 34-byte blocks on both sides), cycling through
+    >= 512 MB of distinct weight copies so that every launch streams its weights from HBM."""
+    from qpu_xla_amd.kernels.quantize import quantize_q8_0
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    per = n * (k // 32) * 34
+    copies = max(2, -(-ROTATION_BYTES // per))
+    runner = Runner(torch, torch.cuda.Stream())
+    weights = []
+    for _ in range(copies):
+        w = torch.randn((n, k), generator=gen, device="cuda", dtype=torch.float32) * 0.02
+        weights.append(quantize_q8_0(w))
+        del w
+    x = torch.randn((rows, k), generator=gen, device="cuda", dtype=torch.float32)
+    xq = quantize_q8_0(x)
+    y = torch.empty((rows, n), dtype=torch.float32, device="cuda")
+    runner.uses(xq, y, *weights)
+    for wq in weights:
+        runner.add("qxt_ggml_q8_0_q8_0_linear", _p(xq), _rs(xq), _p(wq), _rs(wq), _p(y), _rs(y),
+                   rows, k // 32, 0, 0, n, runner.handle)
+    runner.run()
+    torch.cuda.synchronize()
+    times = runner.kernel_times(repeats=2)["q8_0_linear_kernel"]
+    graph = runner.capture()
+    wall_ms, _ = runner.timed_graph(graph, max(2, args.steps // 4), 2)
+    b = q8_linear_bytes(rows, k, n)
+    avg_ms = float(np.mean(times))
+    out = {
+        "shape": f"M={rows} K={k} N={n}",
+        "copies": copies,
+        "rotation_mb": copies * per / 1e6,
+        "bytes_per_launch": b,
+        "kernel_avg_us": avg_ms * 1e3,
+        "kernel_gbs": b / (avg_ms * 1e-3) / 1e9,
+        "kernel_frac_hbm": b / (avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+        "stream_us_per_launch": wall_ms * 1e3 / copies,
+        "stream_gbs": b * copies / (wall_ms * 1e-3) / 1e9,
+    }
+    torch.cuda.synchronize()
+    out["check"] = check_q8_0_q8_0(torch, "q8_0 " + out["shape"], xq, weights[-1], y, rows=tuple(range(rows)))
+    del graph, weights
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     return out
@@ -1095,6 +1169,11 @@ def main() -> int:
         out["cfg2_native_layout"] = [leg_rotated_q4(torch, args, 4, 4096, 11008, 2, "native"),
                                      leg_rotated_q4(torch, args, 4, 4096, 4096, 2, "native")]
         log(f"cfg2: {out['cfg2']}")
+    if "q8_0" in legs:
+        log("leg q8_0 x q8_0 rotated")
+        out["q8_0_q8_0"] = [leg_rotated_q8(torch, args, 1, 2048, 5632, 7), leg_rotated_q8(torch, args, 4, 4096, 11008, 7),
+                            leg_rotated_q8(torch, args, 4, 4096, 4096, 7)]
+        log(f"q8_0 x q8_0: {out['q8_0_q8_0']}")
     if "w8a8" in legs:
         log("leg w8a8 (cfg4)")
         out["w8a8"] = leg_w8a8(torch, args)
@@ -1178,6 +1257,7 @@ def main() -> int:
         "w8a8_gemv": out.get("gemv"),
         "q4_0_prefill": out.get("prefill"),
         "geglu_q8_0": out.get("geglu"),
+        "q8_0_q8_0": out.get("q8_0_q8_0"),
         "shards": out.get("shards"),
         "w8a8_cpu_baseline": cpu_w8a8,
         "decode": decode,

@@ -204,6 +204,153 @@ __global__ __launch_bounds__(kThreads) void q8_0_linear_kernel(Q8Task t) {
     }
 }
 
+// ------------------------------------------------ block-per-lane form
+//
+// Lane l of a wave takes block kw * 64 + l of its columns (kw: the wave's
+// place along K), so one load instruction of a wave reads 64 consecutive
+// 34-byte blocks of one weight row (2,176 contiguous bytes) instead of 64
+// scattered 16-byte pieces of 272-byte units.  Each lane keeps its block of
+// the MR activation rows in registers for the whole launch, the wave walks
+// its columns with the next columns' loads in flight, and the block terms go
+// to LDS for the same ordered sums as the unit form.  Blocks sit at 2-byte
+// offsets: each is read as the aligned dwords around its 32 values (2 x 16
+// bytes + the 2 bytes after them) and its scale, through buffer descriptors
+// whose range turns blocks past K (or a missing row) into zeros.
+
+constexpr uint32_t kOutOfRange = 0x80000000u;  // descriptor ranges are below 2 GiB
+#ifndef QXT_Q8_AHEAD
+#define QXT_Q8_AHEAD 2
+#endif
+#ifndef QXT_Q8_WGS
+#define QXT_Q8_WGS 2
+#endif
+constexpr int kStreamAhead = QXT_Q8_AHEAD;  // columns of loads in flight per wave
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, 0x00020000);
+}
+
+struct Q8StreamTask {
+    const uint8_t *act, *w;
+    float *y;
+    uint32_t act_stride, w_stride, act_extent, w_extent;
+    size_t y_stride;
+    int rows, blocks, wcol0, ocol0, ncols, cpw, wk;  // wk: waves along K (blocks <= 64 * wk)
+};
+
+// One block's raw words: 8 aligned dwords around the values, the 2 bytes
+// after them, the scale bits and the byte shift (0 or 2) that realigns them.
+struct RawBlock {
+    uint32_t w[8];
+    uint32_t tail, sbits, shift;
+};
+
+__device__ __forceinline__ void load_block(__amdgpu_buffer_rsrc_t r, uint32_t o, RawBlock &b) {
+    const uint32_t v = (o + 2) & ~3u;  // the 32 values start 2 bytes into the block
+    const v4u x0 = __builtin_amdgcn_raw_buffer_load_b128(r, v, 0, 0);
+    const v4u x1 = __builtin_amdgcn_raw_buffer_load_b128(r, v + 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        b.w[i] = x0[i];
+        b.w[4 + i] = x1[i];
+    }
+    // 16-bit loads for the 2 bytes past the values and for the scale: a
+    // 32-bit load ending past the last block of a tensor would read as zero.
+    b.tail = __builtin_amdgcn_raw_buffer_load_b16(r, v + 32, 0, 0);
+    b.sbits = __builtin_amdgcn_raw_buffer_load_b16(r, o, 0, 0);
+    b.shift = (o + 2) & 3u;
+}
+
+__device__ __forceinline__ void block_values(const RawBlock &b, uint32_t (&qs)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qs[i] = __builtin_amdgcn_alignbyte(i < 7 ? b.w[i + 1] : b.tail, b.w[i], b.shift);
+}
+
+template <int MR>
+__global__ __launch_bounds__(kThreads) void q8_0_stream_kernel(Q8StreamTask t) {
+    extern __shared__ int lds[];
+    float *cb = reinterpret_cast<float *>(lds);  // [MR][cpw][cbs] block terms
+    const int cbs = ((t.blocks + 3) & ~3) + 4;  // float4-aligned rows, padded
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int kw = wave % t.wk, cg = wave / t.wk, groups = (kThreads / 64) / t.wk;
+    const int b = kw * 64 + lane;
+    const bool in_k = b < t.blocks;
+    const int col_base = blockIdx.x * t.cpw;
+    const int r0 = blockIdx.y * MR;
+    const int tile_cols = min(t.cpw, t.ncols - col_base);
+    const __amdgpu_buffer_rsrc_t ra = rsrc(t.act, t.act_extent);
+    const __amdgpu_buffer_rsrc_t rw = rsrc(t.w, t.w_extent);
+
+    auto w_offset = [&](int col) -> uint32_t {
+        return in_k && col < tile_cols
+                   ? static_cast<uint32_t>(t.wcol0 + col_base + col) * t.w_stride + static_cast<uint32_t>(b) * 34u
+                   : kOutOfRange;
+    };
+    // The first columns' weights are requested before the activation.
+    RawBlock ring[kStreamAhead];
+#pragma unroll
+    for (int j = 0; j < kStreamAhead; ++j) load_block(rw, w_offset(cg + j * groups), ring[j]);
+
+    uint32_t a[MR][8];
+    float da[MR];
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+        RawBlock ab;
+        load_block(ra, in_k && r0 + r < t.rows
+                           ? static_cast<uint32_t>(r0 + r) * t.act_stride + static_cast<uint32_t>(b) * 34u
+                           : kOutOfRange,
+                   ab);
+        block_values(ab, a[r]);
+        da[r] = half_bits_to_float(ab.sbits);
+    }
+
+    // Columns cg, cg + groups, ... of the tile; slot j of the ring holds the
+    // column of step s with s % kStreamAhead == j.
+    const int steps = (tile_cols - cg + groups - 1) / groups;
+    for (int s0 = 0; s0 < steps; s0 += kStreamAhead) {
+#pragma unroll
+        for (int j = 0; j < kStreamAhead; ++j) {
+            const int s = s0 + j;
+            if (s >= steps) break;
+            const int col = cg + s * groups;
+            uint32_t qs[8];
+            block_values(ring[j], qs);
+            const float dw = half_bits_to_float(ring[j].sbits);
+            load_block(rw, w_offset(col + kStreamAhead * groups), ring[j]);
+            if (in_k) {
+#pragma unroll
+                for (int r = 0; r < MR; ++r) {
+                    int dot = 0;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) dot = dot4(static_cast<int>(qs[i]), static_cast<int>(a[r][i]), dot);
+                    cb[(r * t.cpw + col) * cbs + b] = block_term(dot, da[r], dw);
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // One thread per (row, column): the column's block terms in block order.
+    for (int k = threadIdx.x; k < MR * tile_cols; k += kThreads) {
+        const int r = k / tile_cols;
+        const int col = k - r * tile_cols;
+        if (r0 + r >= t.rows) continue;
+        const float *c = cb + (r * t.cpw + col) * cbs;
+        float acc = 0.0f;
+        int i = 0;
+        for (; i + 4 <= t.blocks; i += 4) {
+            const float4 v = *reinterpret_cast<const float4 *>(c + i);
+            acc += v.x;
+            acc += v.y;
+            acc += v.z;
+            acc += v.w;
+        }
+        for (; i < t.blocks; ++i) acc += c[i];
+        float *out = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(t.y) + (r0 + r) * t.y_stride);
+        out[t.ocol0 + col_base + col] = acc;
+    }
+}
+
 template <int MR>
 int launch_q8(Q8Task t, hipStream_t stream) {
     const bool fast = t.blocks % 8 == 0 && aligned(t.w, 16) && t.w_stride % 16 == 0;
@@ -224,6 +371,57 @@ int launch_q8(Q8Task t, hipStream_t stream) {
     dim3 grid((t.ncols + cpw - 1) / cpw, row_groups, 1);
     if (fast) return launch("q8_0_linear_kernel", q8_0_linear_kernel<MR, true>, grid, dim3(kThreads), lds, stream, t);
     return launch("q8_0_linear_kernel", q8_0_linear_kernel<MR, false>, grid, dim3(kThreads), lds, stream, t);
+}
+
+// The block-per-lane form for K <= 256 blocks (8192 values) with operands
+// below 2 GiB; QXT_CAPABILITY_MISSING otherwise (the caller then takes the
+// unit form).
+template <int MR>
+int launch_q8_stream(const Q8Task &u, hipStream_t stream) {
+    if (u.blocks > 256) return QXT_CAPABILITY_MISSING;
+    const uint64_t a_extent = static_cast<uint64_t>(u.rows - 1) * u.act_stride + static_cast<uint64_t>(u.blocks) * 34;
+    const uint64_t w_extent =
+        static_cast<uint64_t>(u.wcol0 + u.ncols - 1) * u.w_stride + static_cast<uint64_t>(u.blocks) * 34;
+    if (a_extent >= (1ull << 31) || w_extent >= (1ull << 31)) return QXT_CAPABILITY_MISSING;
+    Q8StreamTask t{};
+    t.act = u.act;
+    t.w = u.w;
+    t.y = u.y;
+    t.act_stride = static_cast<uint32_t>(u.act_stride);
+    t.w_stride = static_cast<uint32_t>(u.w_stride);
+    t.act_extent = static_cast<uint32_t>(a_extent);
+    t.w_extent = static_cast<uint32_t>(w_extent);
+    t.y_stride = u.y_stride;
+    t.rows = u.rows;
+    t.blocks = u.blocks;
+    t.wcol0 = u.wcol0;
+    t.ocol0 = u.ocol0;
+    t.ncols = u.ncols;
+    t.wk = u.blocks <= 64 ? 1 : u.blocks <= 128 ? 2 : 4;
+    const int groups = (kThreads / 64) / t.wk;
+    const int row_groups = (u.rows + MR - 1) / MR;
+    // Two workgroups per CU, whole column groups per workgroup.
+    const long want = static_cast<long>(QXT_Q8_WGS) * compute_units();
+    int cpw = static_cast<int>((static_cast<long>(u.ncols) * row_groups + want - 1) / want);
+    cpw = std::min(64, std::max(groups, (cpw + groups - 1) / groups * groups));
+    const int cbs = ((u.blocks + 3) & ~3) + 4;
+    const size_t lds = static_cast<size_t>(MR) * cpw * cbs * 4;
+    if (lds > kMaxLds) return QXT_CAPABILITY_MISSING;
+    t.cpw = cpw;
+    const dim3 grid((u.ncols + cpw - 1) / cpw, row_groups, 1);
+    return launch("q8_0_linear_kernel", q8_0_stream_kernel<MR>, grid, dim3(kThreads), lds, stream, t);
+}
+
+template <int MR>
+int dispatch_q8(const Q8Task &t, hipStream_t stream) {
+#ifndef QXT_Q8_STREAM
+#define QXT_Q8_STREAM 1
+#endif
+    if (QXT_Q8_STREAM) {
+        const int rc = launch_q8_stream<MR>(t, stream);
+        if (rc != QXT_CAPABILITY_MISSING) return rc;
+    }
+    return launch_q8<MR>(t, stream);
 }
 
 }  // namespace
@@ -267,9 +465,9 @@ extern "C" int qxt_ggml_q8_0_q8_0_linear(const void *activation, size_t activati
     t.ncols = static_cast<int>(column_count);
     const hipStream_t s = as_stream(stream);
     switch (rows >= 4 ? 4 : rows) {
-        case 1: return launch_q8<1>(t, s);
-        case 2: return launch_q8<2>(t, s);
-        case 3: return launch_q8<3>(t, s);
-        default: return launch_q8<4>(t, s);
+        case 1: return dispatch_q8<1>(t, s);
+        case 2: return dispatch_q8<2>(t, s);
+        case 3: return dispatch_q8<3>(t, s);
+        default: return dispatch_q8<4>(t, s);
     }
 }

@@ -364,3 +364,28 @@ def test_geglu_on_unaligned_rows_every_output_layout(rows: int, columns: int) ->
         scales, values = geglu.ggml_geglu_q8_0_split(gate_d, up_d, scales=scales)
         np.testing.assert_array_equal(scales.cpu().numpy().view(view).astype(np.uint32), words)
         np.testing.assert_array_equal(values.cpu().numpy(), planes)
+
+
+@pytest.mark.parametrize("rows,blocks,n,wcol0,ncols", [
+    (4, 8, 96, 0, 96),        # 8 blocks: one wave along K, lanes 8..63 idle
+    (4, 32, 200, 5, 190),     # ragged last tile, weight column offset
+    (5, 64, 300, 3, 290),     # 64 blocks (one wave along K); the second row group has one row
+    (8, 128, 520, 0, 520),    # 128 blocks: two waves along K, two full row groups
+    (4, 176, 70, 0, 70),      # 176 blocks: four waves along K, the last one idle
+    (3, 256, 40, 0, 40),      # 256 blocks (K = 8192): the largest block-per-lane K
+    (4, 264, 40, 0, 40),      # 264 blocks: past it, the unit form
+])
+def test_q8_0_linear_block_per_lane_forms(rows: int, blocks: int, n: int, wcol0: int, ncols: int) -> None:
+    # Up to 256 blocks the Q8_0 x Q8_0 linear takes one block per lane (one,
+    # two or four waves along K, the activation blocks in registers); beyond,
+    # units of eight blocks per thread.  Both sum the same block terms in
+    # block order.
+    from qpu_xla_amd.kernels import ggml_q8_0 as q8
+
+    act, wt = _q8_operands(5400 + rows + blocks, rows, n, blocks)
+    out = torch.full((rows, ncols + 16), float(SENTINEL), device="cuda")
+    q8.ggml_q8_0_q8_0_linear(dev(act), dev(wt), out, weight_column_start=wcol0, output_column_start=16,
+                             column_count=ncols)
+    got = out.cpu().numpy()
+    np.testing.assert_array_equal(got[:, :16], SENTINEL)
+    np.testing.assert_array_equal(got[:, 16:], oracle.q8_0_q8_0_reference(act, wt[wcol0:wcol0 + ncols]))
