@@ -134,19 +134,19 @@ struct BandLookup {
 // 5632: 10-12 % faster than one block at a time).
 constexpr int kGegluBlocks = 2;
 
-// Blocks first, first + stride, ... (kGegluBlocks of them, those < total) for
+// Blocks first, first + stride, ... (NB of them, those < total) for
 // one 8-lane group: each lane reads float4 of gate and of up per block,
 // v = fl32(gelu * up), and the block is quantised by the Q8_0 rule of
 // ggml_geglu_q8.py:50-55: d = absmax / 127, inverse = 1 / d (0 when d is 0),
 // q = clip(rint(v * inverse), +-127), d stored as fp16.
-template <bool VEC, int LAYOUT, typename Lookup>
+template <bool VEC, int LAYOUT, int NB, typename Lookup>
 __device__ __forceinline__ void geglu_blocks(uint64_t first, uint64_t stride, uint64_t total, int l8,
                                              const float *__restrict__ gate, size_t gate_stride,
                                              const float *__restrict__ up, size_t up_stride, const Lookup &lookup,
                                              const Q8Planes &out, uint32_t blocks) {
-    float4 g[kGegluBlocks], u[kGegluBlocks];
+    float4 g[NB], u[NB];
 #pragma unroll
-    for (int i = 0; i < kGegluBlocks; ++i) {
+    for (int i = 0; i < NB; ++i) {
         const uint64_t gb = first + i * stride;
         if (gb < total) {
             const uint32_t row = static_cast<uint32_t>(gb / blocks);
@@ -158,7 +158,7 @@ __device__ __forceinline__ void geglu_blocks(uint64_t first, uint64_t stride, ui
         }
     }
 #pragma unroll
-    for (int i = 0; i < kGegluBlocks; ++i) {
+    for (int i = 0; i < NB; ++i) {
         const uint64_t gb = first + i * stride;
         if (gb >= total) break;  // whole 8-lane groups leave together
         const uint32_t row = static_cast<uint32_t>(gb / blocks);
@@ -199,7 +199,7 @@ __global__ __launch_bounds__(kThreads) void geglu_q8_0_kernel(const float *__res
                                                               uint32_t rows, uint32_t blocks) {
     const uint64_t groups = (static_cast<uint64_t>(gridDim.x) * kThreads) >> 3;
     const uint64_t first = (static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x) >> 3;
-    geglu_blocks<VEC, LAYOUT>(first, groups, static_cast<uint64_t>(rows) * blocks, threadIdx.x & 7, gate,
+    geglu_blocks<VEC, LAYOUT, kGegluBlocks>(first, groups, static_cast<uint64_t>(rows) * blocks, threadIdx.x & 7, gate,
                               gate_stride, up, up_stride, TableLookup{table}, out, blocks);
 }
 
@@ -213,7 +213,12 @@ constexpr int kBandThreads = 1024;
 constexpr int kBandWorkgroupsPerCU = 2;       // 2 x 52 KB of the 160 KB LDS, 32 waves per CU
 constexpr uint64_t kBandMinBlocks = 1u << 16;  // below this the gather kernel is as fast
 
-template <bool VEC, int LAYOUT>
+// NB blocks per 8-lane group and pass: 2 for the largest jobs, 1 below
+// kBandTwoBlocks (measured on MI355X at K = 5632: M = 512 9.0 -> 8.0 us with
+// one, M = 2048 21.2 -> 21.6 us).
+constexpr uint64_t kBandTwoBlocks = 1u << 18;
+
+template <bool VEC, int LAYOUT, int NB>
 __global__ __launch_bounds__(kBandThreads) void geglu_q8_0_band_kernel(
     const float *__restrict__ gate, size_t gate_stride, const float *__restrict__ up, size_t up_stride,
     const uint16_t *__restrict__ table, Q8Planes out, uint32_t rows, uint32_t blocks) {
@@ -233,9 +238,9 @@ __global__ __launch_bounds__(kBandThreads) void geglu_q8_0_band_kernel(
     const uint64_t groups = static_cast<uint64_t>(gridDim.x) * (kBandThreads / 8);
     const uint64_t first = static_cast<uint64_t>(blockIdx.x) * (kBandThreads / 8) + (threadIdx.x >> 3);
     const BandLookup lookup{band, table};
-    for (uint64_t base = first; base < total; base += groups * kGegluBlocks)
-        geglu_blocks<VEC, LAYOUT>(base, groups, total, threadIdx.x & 7, gate, gate_stride, up, up_stride, lookup,
-                                  out, blocks);
+    for (uint64_t base = first; base < total; base += groups * NB)
+        geglu_blocks<VEC, LAYOUT, NB>(base, groups, total, threadIdx.x & 7, gate, gate_stride, up, up_stride, lookup,
+                                      out, blocks);
 }
 
 // ------------------------------------------------------------- per-row int8
@@ -419,14 +424,15 @@ int launch_geglu(const float *gate, size_t gate_stride, const float *up, size_t 
     const bool vec = aligned(gate, 16) && gate_stride % 16 == 0 && aligned(up, 16) && up_stride % 16 == 0;
     const uint64_t total = static_cast<uint64_t>(rows) * blocks;
     if (total >= kBandMinBlocks && aligned(table, 16)) {
-        const uint64_t per_workgroup = static_cast<uint64_t>(kBandThreads / 8) * kGegluBlocks;
+        const bool two = total >= kBandTwoBlocks;
+        const uint64_t per_workgroup = static_cast<uint64_t>(kBandThreads / 8) * (two ? 2 : 1);
         const uint64_t wanted = (total + per_workgroup - 1) / per_workgroup;
         const uint64_t resident = static_cast<uint64_t>(compute_units()) * kBandWorkgroupsPerCU;
         const unsigned grid = static_cast<unsigned>(wanted < resident ? wanted : resident);
-        return launch("geglu_q8_0_band_kernel",
-                      vec ? geglu_q8_0_band_kernel<true, LAYOUT> : geglu_q8_0_band_kernel<false, LAYOUT>, dim3(grid),
-                      dim3(kBandThreads), 0, as_stream(stream), gate, gate_stride, up, up_stride, table, out, rows,
-                      blocks);
+        auto kernel = vec ? (two ? geglu_q8_0_band_kernel<true, LAYOUT, 2> : geglu_q8_0_band_kernel<true, LAYOUT, 1>)
+                          : (two ? geglu_q8_0_band_kernel<false, LAYOUT, 2> : geglu_q8_0_band_kernel<false, LAYOUT, 1>);
+        return launch("geglu_q8_0_band_kernel", kernel, dim3(grid), dim3(kBandThreads), 0, as_stream(stream), gate,
+                      gate_stride, up, up_stride, table, out, rows, blocks);
     }
     const unsigned grid = grid_for_blocks((total + kGegluBlocks - 1) / kGegluBlocks);
     return launch("geglu_q8_0_kernel", vec ? geglu_q8_0_kernel<true, LAYOUT> : geglu_q8_0_kernel<false, LAYOUT>,

@@ -389,3 +389,23 @@ def test_q8_0_linear_block_per_lane_forms(rows: int, blocks: int, n: int, wcol0:
     got = out.cpu().numpy()
     np.testing.assert_array_equal(got[:, :16], SENTINEL)
     np.testing.assert_array_equal(got[:, 16:], oracle.q8_0_q8_0_reference(act, wt[wcol0:wcol0 + ncols]))
+
+
+def test_geglu_band_two_blocks_per_pass_every_output_layout() -> None:
+    # At least 2^18 blocks: the band kernel takes two blocks per 8-lane group
+    # and pass (fewer take one, as every smaller GEGLU case here).
+    from qpu_xla_amd.kernels import ggml_geglu_q8 as geglu
+
+    rows, columns = 1600, 5632
+    assert rows * columns // 32 >= 1 << 18
+    rng = np.random.default_rng(5501)
+    gate = rng.normal(0.0, 1.0, (rows, columns)).astype(np.float32)
+    up = rng.normal(0.0, 1.0, (rows, columns)).astype(np.float32)
+    np.testing.assert_array_equal(geglu.ggml_geglu_q8_0(dev(gate), dev(up)).cpu().numpy(),
+                                  oracle.geglu_q8_0_reference(gate, up))
+    words, planes = oracle.geglu_q8_0_split_reference(gate, up)
+    for dtype, view in ((torch.int32, np.uint32), (torch.int16, np.uint16)):
+        scales = torch.empty((rows, columns // 32), dtype=dtype, device="cuda")
+        scales, values = geglu.ggml_geglu_q8_0_split(dev(gate), dev(up), scales=scales)
+        np.testing.assert_array_equal(scales.cpu().numpy().view(view).astype(np.uint32), words)
+        np.testing.assert_array_equal(values.cpu().numpy(), planes)
