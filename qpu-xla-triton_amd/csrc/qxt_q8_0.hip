@@ -207,10 +207,11 @@ __global__ __launch_bounds__(kThreads) void q8_0_linear_kernel(Q8Task t) {
 // ------------------------------------------------ block-per-lane form
 //
 // Lane l of a wave takes block kw * 64 + l of its columns (kw: the wave's
-// place along K), so one load instruction of a wave reads 64 consecutive
-// 34-byte blocks of one weight row (2,176 contiguous bytes) instead of 64
-// scattered 16-byte pieces of 272-byte units.  Each lane keeps its block of
-// the MR activation rows in registers for the whole launch, the wave walks
+// place along K; past 256 blocks also block kw * 64 + l + 256), so one load
+// instruction of a wave reads 64 consecutive 34-byte blocks of one weight
+// row (2,176 contiguous bytes) instead of 64 scattered 16-byte pieces of
+// 272-byte units.  Each lane keeps its blocks of the MR activation rows in
+// registers for the whole launch, the wave walks
 // its columns with the next columns' loads in flight, and the block terms go
 // to LDS for the same ordered sums as the unit form.  Blocks sit at 2-byte
 // offsets: each is read as the aligned dwords around its 32 values (2 x 16
@@ -266,43 +267,53 @@ __device__ __forceinline__ void block_values(const RawBlock &b, uint32_t (&qs)[8
     for (int i = 0; i < 8; ++i) qs[i] = __builtin_amdgcn_alignbyte(i < 7 ? b.w[i + 1] : b.tail, b.w[i], b.shift);
 }
 
-template <int MR>
+template <int MR, int C>
 __global__ __launch_bounds__(kThreads) void q8_0_stream_kernel(Q8StreamTask t) {
     extern __shared__ int lds[];
     float *cb = reinterpret_cast<float *>(lds);  // [MR][cpw][cbs] block terms
     const int cbs = ((t.blocks + 3) & ~3) + 4;  // float4-aligned rows, padded
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int kw = wave % t.wk, cg = wave / t.wk, groups = (kThreads / 64) / t.wk;
-    const int b = kw * 64 + lane;
-    const bool in_k = b < t.blocks;
+    // Blocks b[c] = kw * 64 + lane + c * 64 * wk: C blocks of each column per lane.
+    int b[C];
+    bool in_k[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        b[c] = kw * 64 + lane + c * 64 * t.wk;
+        in_k[c] = b[c] < t.blocks;
+    }
     const int col_base = blockIdx.x * t.cpw;
     const int r0 = blockIdx.y * MR;
     const int tile_cols = min(t.cpw, t.ncols - col_base);
     const __amdgpu_buffer_rsrc_t ra = rsrc(t.act, t.act_extent);
     const __amdgpu_buffer_rsrc_t rw = rsrc(t.w, t.w_extent);
 
-    auto w_offset = [&](int col) -> uint32_t {
-        return in_k && col < tile_cols
-                   ? static_cast<uint32_t>(t.wcol0 + col_base + col) * t.w_stride + static_cast<uint32_t>(b) * 34u
+    auto w_offset = [&](int col, int c) -> uint32_t {
+        return in_k[c] && col < tile_cols
+                   ? static_cast<uint32_t>(t.wcol0 + col_base + col) * t.w_stride + static_cast<uint32_t>(b[c]) * 34u
                    : kOutOfRange;
     };
     // The first columns' weights are requested before the activation.
-    RawBlock ring[kStreamAhead];
+    RawBlock ring[kStreamAhead][C];
 #pragma unroll
-    for (int j = 0; j < kStreamAhead; ++j) load_block(rw, w_offset(cg + j * groups), ring[j]);
+    for (int j = 0; j < kStreamAhead; ++j)
+#pragma unroll
+        for (int c = 0; c < C; ++c) load_block(rw, w_offset(cg + j * groups, c), ring[j][c]);
 
-    uint32_t a[MR][8];
-    float da[MR];
+    uint32_t a[C][MR][8];
+    float da[C][MR];
 #pragma unroll
-    for (int r = 0; r < MR; ++r) {
-        RawBlock ab;
-        load_block(ra, in_k && r0 + r < t.rows
-                           ? static_cast<uint32_t>(r0 + r) * t.act_stride + static_cast<uint32_t>(b) * 34u
-                           : kOutOfRange,
-                   ab);
-        block_values(ab, a[r]);
-        da[r] = half_bits_to_float(ab.sbits);
-    }
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+            RawBlock ab;
+            load_block(ra, in_k[c] && r0 + r < t.rows
+                               ? static_cast<uint32_t>(r0 + r) * t.act_stride + static_cast<uint32_t>(b[c]) * 34u
+                               : kOutOfRange,
+                       ab);
+            block_values(ab, a[c][r]);
+            da[c][r] = half_bits_to_float(ab.sbits);
+        }
 
     // Columns cg, cg + groups, ... of the tile; slot j of the ring holds the
     // column of step s with s % kStreamAhead == j.
@@ -313,17 +324,21 @@ __global__ __launch_bounds__(kThreads) void q8_0_stream_kernel(Q8StreamTask t) {
             const int s = s0 + j;
             if (s >= steps) break;
             const int col = cg + s * groups;
-            uint32_t qs[8];
-            block_values(ring[j], qs);
-            const float dw = half_bits_to_float(ring[j].sbits);
-            load_block(rw, w_offset(col + kStreamAhead * groups), ring[j]);
-            if (in_k) {
 #pragma unroll
-                for (int r = 0; r < MR; ++r) {
-                    int dot = 0;
+            for (int c = 0; c < C; ++c) {
+                uint32_t qs[8];
+                block_values(ring[j][c], qs);
+                const float dw = half_bits_to_float(ring[j][c].sbits);
+                load_block(rw, w_offset(col + kStreamAhead * groups, c), ring[j][c]);
+                if (in_k[c]) {
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) dot = dot4(static_cast<int>(qs[i]), static_cast<int>(a[r][i]), dot);
-                    cb[(r * t.cpw + col) * cbs + b] = block_term(dot, da[r], dw);
+                    for (int r = 0; r < MR; ++r) {
+                        int dot = 0;
+#pragma unroll
+                        for (int i = 0; i < 8; ++i)
+                            dot = dot4(static_cast<int>(qs[i]), static_cast<int>(a[c][r][i]), dot);
+                        cb[(r * t.cpw + col) * cbs + b[c]] = block_term(dot, da[c][r], dw);
+                    }
                 }
             }
         }
@@ -373,12 +388,12 @@ int launch_q8(Q8Task t, hipStream_t stream) {
     return launch("q8_0_linear_kernel", q8_0_linear_kernel<MR, false>, grid, dim3(kThreads), lds, stream, t);
 }
 
-// The block-per-lane form for K <= 256 blocks (8192 values) with operands
-// below 2 GiB; QXT_CAPABILITY_MISSING otherwise (the caller then takes the
-// unit form).
+// The block-per-lane form for K <= 512 blocks (16384 values; beyond 256
+// blocks each lane takes two) with operands below 2 GiB;
+// QXT_CAPABILITY_MISSING otherwise (the caller then takes the unit form).
 template <int MR>
 int launch_q8_stream(const Q8Task &u, hipStream_t stream) {
-    if (u.blocks > 256) return QXT_CAPABILITY_MISSING;
+    if (u.blocks > 512) return QXT_CAPABILITY_MISSING;
     const uint64_t a_extent = static_cast<uint64_t>(u.rows - 1) * u.act_stride + static_cast<uint64_t>(u.blocks) * 34;
     const uint64_t w_extent =
         static_cast<uint64_t>(u.wcol0 + u.ncols - 1) * u.w_stride + static_cast<uint64_t>(u.blocks) * 34;
@@ -397,7 +412,7 @@ int launch_q8_stream(const Q8Task &u, hipStream_t stream) {
     t.wcol0 = u.wcol0;
     t.ocol0 = u.ocol0;
     t.ncols = u.ncols;
-    t.wk = u.blocks <= 64 ? 1 : u.blocks <= 128 ? 2 : 4;
+    t.wk = u.blocks <= 64 ? 1 : u.blocks <= 128 ? 2 : 4;  // beyond 256 blocks: 2 per lane
     const int groups = (kThreads / 64) / t.wk;
     const int row_groups = (u.rows + MR - 1) / MR;
     // Two workgroups per CU, whole column groups per workgroup.
@@ -405,11 +420,16 @@ int launch_q8_stream(const Q8Task &u, hipStream_t stream) {
     int cpw = static_cast<int>((static_cast<long>(u.ncols) * row_groups + want - 1) / want);
     cpw = std::min(64, std::max(groups, (cpw + groups - 1) / groups * groups));
     const int cbs = ((u.blocks + 3) & ~3) + 4;
+    // At most kMaxLds of block terms (whole column groups).
+    const int lds_cols = static_cast<int>(kMaxLds / (static_cast<size_t>(MR) * cbs * 4)) / groups * groups;
+    if (lds_cols < groups) return QXT_CAPABILITY_MISSING;
+    cpw = std::min(cpw, lds_cols);
     const size_t lds = static_cast<size_t>(MR) * cpw * cbs * 4;
-    if (lds > kMaxLds) return QXT_CAPABILITY_MISSING;
     t.cpw = cpw;
     const dim3 grid((u.ncols + cpw - 1) / cpw, row_groups, 1);
-    return launch("q8_0_linear_kernel", q8_0_stream_kernel<MR>, grid, dim3(kThreads), lds, stream, t);
+    if (u.blocks > 256)
+        return launch("q8_0_linear_kernel", q8_0_stream_kernel<MR, 2>, grid, dim3(kThreads), lds, stream, t);
+    return launch("q8_0_linear_kernel", q8_0_stream_kernel<MR, 1>, grid, dim3(kThreads), lds, stream, t);
 }
 
 template <int MR>

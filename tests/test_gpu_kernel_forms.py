@@ -372,14 +372,17 @@ def test_geglu_on_unaligned_rows_every_output_layout(rows: int, columns: int) ->
     (5, 64, 300, 3, 290),     # 64 blocks (one wave along K); the second row group has one row
     (8, 128, 520, 0, 520),    # 128 blocks: two waves along K, two full row groups
     (4, 176, 70, 0, 70),      # 176 blocks: four waves along K, the last one idle
-    (3, 256, 40, 0, 40),      # 256 blocks (K = 8192): the largest block-per-lane K
-    (4, 264, 40, 0, 40),      # 264 blocks: past it, the unit form
+    (3, 256, 40, 0, 40),      # 256 blocks (K = 8192): the largest with one block per lane
+    (4, 264, 40, 0, 40),      # 264 blocks: two per lane, the second only for lanes 0..7 of wave 0
+    (2, 344, 120, 7, 100),    # K = 11008 (a down projection), two blocks per lane
+    (1, 512, 64, 0, 64),      # 512 blocks (K = 16384): the largest block-per-lane K
+    (1, 520, 40, 0, 40),      # 520 blocks: past it, the unit form (one row: its LDS holds 4 rows only to K = 12288)
 ])
 def test_q8_0_linear_block_per_lane_forms(rows: int, blocks: int, n: int, wcol0: int, ncols: int) -> None:
-    # Up to 256 blocks the Q8_0 x Q8_0 linear takes one block per lane (one,
-    # two or four waves along K, the activation blocks in registers); beyond,
-    # units of eight blocks per thread.  Both sum the same block terms in
-    # block order.
+    # Up to 512 blocks the Q8_0 x Q8_0 linear takes one block per lane (one,
+    # two or four waves along K, two blocks per lane past 256, the activation
+    # blocks in registers); beyond, units of eight blocks per thread.  Both
+    # sum the same block terms in block order.
     from qpu_xla_amd.kernels import ggml_q8_0 as q8
 
     act, wt = _q8_operands(5400 + rows + blocks, rows, n, blocks)
