@@ -18,9 +18,11 @@ Also reported on the same JSON line:
                          and over the native ggml rows);
   * ``q8_0_q8_0``     -- the Q8_0 x Q8_0 linear (native blocks) at M = 1 and M = 4 decode
                          shapes, rotated weights, in GB/s against the HBM peak;
+  * ``q4_0_long_rows``-- Q4_0 linears over native rows of 176 to 448 blocks (K = 5632 to
+                         14336) at M = 1 to 4, rotated weights;
   * ``cpu_baseline``  -- the NumPy oracle of the reference CPU path on this host.
 
-Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--legs decode,w8a8,gemv,prefill,geglu,q8_0,shards,cfg0,cfg1,cfg2,copy,cpu]
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--legs decode,w8a8,gemv,prefill,geglu,q8_0,q4_long,shards,cfg0,cfg1,cfg2,copy,cpu]
 Weights and activations are synthetic (seeded random, the BASELINE distributions).
 """
 
@@ -71,7 +73,7 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--legs", default="decode,w8a8,gemv,prefill,geglu,q8_0,shards,cfg0,cfg1,cfg2,copy,cpu")
+    ap.add_argument("--legs", default="decode,w8a8,gemv,prefill,geglu,q8_0,q4_long,shards,cfg0,cfg1,cfg2,copy,cpu")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of each CPU-baseline sample")
     return ap.parse_args()
 
@@ -1169,6 +1171,12 @@ def main() -> int:
         out["cfg2_native_layout"] = [leg_rotated_q4(torch, args, 4, 4096, 11008, 2, "native"),
                                      leg_rotated_q4(torch, args, 4, 4096, 4096, 2, "native")]
         log(f"cfg2: {out['cfg2']}")
+    if "q4_long" in legs:
+        log("leg q4_0 long rows (native layout)")
+        out["q4_0_long_rows"] = [leg_rotated_q4(torch, args, m, k, n, 8, "native")
+                                 for m, k, n in ((2, 5632, 2048), (4, 5632, 2048), (1, 11008, 4096),
+                                                 (4, 11008, 4096), (4, 14336, 4096))]
+        log(f"q4_0 long rows: {out['q4_0_long_rows']}")
     if "q8_0" in legs:
         log("leg q8_0 x q8_0 rotated")
         out["q8_0_q8_0"] = [leg_rotated_q8(torch, args, 1, 2048, 5632, 7), leg_rotated_q8(torch, args, 4, 4096, 11008, 7),
@@ -1258,6 +1266,7 @@ def main() -> int:
         "q4_0_prefill": out.get("prefill"),
         "geglu_q8_0": out.get("geglu"),
         "q8_0_q8_0": out.get("q8_0_q8_0"),
+        "q4_0_long_rows": out.get("q4_0_long_rows"),
         "shards": out.get("shards"),
         "w8a8_cpu_baseline": cpu_w8a8,
         "decode": decode,

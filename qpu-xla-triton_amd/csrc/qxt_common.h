@@ -76,6 +76,15 @@ int q4_0_tiled_native(const void *activation, size_t activation_row_stride, cons
                       uint32_t blocks, uint32_t weight_column_start, uint32_t output_column_start,
                       uint32_t column_count, hipStream_t stream);
 
+// Native-layout Q4_0 x Q8_0 linear for 1..15 rows and K <= 24576 with blocks
+// spread one per lane (qxt_q4_0_stream.hip); same contract and result as the
+// small-M kernel.  QXT_CAPABILITY_MISSING (no message, nothing launched) for
+// shapes it does not take.
+int q4_0_stream_native(const void *activation, size_t activation_row_stride, const void *weight,
+                       size_t weight_row_stride, float *destination, size_t destination_row_stride, uint32_t rows,
+                       uint32_t blocks, uint32_t weight_column_start, uint32_t output_column_start,
+                       uint32_t column_count, hipStream_t stream);
+
 // QXT_OK when a Q4_0 linear of `rows` rows and `blocks` blocks fits the LDS of
 // one workgroup on the v_dot4 path, else QXT_CAPABILITY_MISSING with a
 // message (qxt_q4_0.hip).

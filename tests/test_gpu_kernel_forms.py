@@ -412,3 +412,34 @@ def test_geglu_band_two_blocks_per_pass_every_output_layout() -> None:
         scales, values = geglu.ggml_geglu_q8_0_split(dev(gate), dev(up), scales=scales)
         np.testing.assert_array_equal(scales.cpu().numpy().view(view).astype(np.uint32), words)
         np.testing.assert_array_equal(values.cpu().numpy(), planes)
+
+
+@pytest.mark.parametrize("rows,blocks,n,wcol0,ncols,weight_offset", [
+    (1, 129, 64, 0, 64, 0),     # the first block count past 128: one block per lane, four waves along K
+    (2, 176, 2048, 0, 2048, 0),  # K = 5632 (TinyLlama down), two rows
+    (4, 256, 100, 3, 90, 0),    # K = 8192, the last count with one block per lane
+    (3, 257, 40, 0, 40, 2),     # two blocks per lane; weights 2 bytes past a 16-byte boundary
+    (4, 344, 300, 10, 280, 0),  # K = 11008 (Llama-7B down), four rows
+    (5, 448, 70, 0, 70, 0),     # K = 14336, a second row group of one row
+    (1, 513, 40, 0, 40, 0),     # three blocks per lane
+    (4, 768, 33, 0, 33, 0),     # K = 24576: the largest spread over lanes
+    (1, 776, 40, 0, 40, 0),     # past it: the unit kernels
+])
+def test_q4_0_native_linear_long_rows_blocks_spread_over_lanes(rows: int, blocks: int, n: int, wcol0: int, ncols: int,
+                                                               weight_offset: int) -> None:
+    # Native Q4_0 rows of more than 128 blocks with up to 15 activation rows:
+    # each lane takes blocks kw * 64 + l (+ 256, + 512), the activation blocks
+    # and -8 * sum(a) in registers; the block terms are summed in block order.
+    rng = np.random.default_rng(5600 + rows * 7 + blocks)
+    w = (rng.standard_normal((n, blocks * 32), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    wq = oracle.quantize_q4_0_blocks(w)
+    act = oracle.quantize_q8_0_blocks(rng.standard_normal((rows, blocks * 32), dtype=np.float32))
+    storage = torch.zeros(wq.size + weight_offset, dtype=torch.uint8, device="cuda")
+    weight = storage[weight_offset:].view(wq.shape)
+    weight.copy_(torch.from_numpy(wq))
+    out = torch.full((rows, ncols + 16), float(SENTINEL), device="cuda")
+    ggml_q4_0_q8_0_linear(dev(act), weight, out, weight_column_start=wcol0, output_column_start=16,
+                          column_count=ncols)
+    got = out.cpu().numpy()
+    np.testing.assert_array_equal(got[:, :16], SENTINEL)
+    np.testing.assert_array_equal(got[:, 16:], oracle.q4_0_q8_0_reference(act, wq[wcol0:wcol0 + ncols]))
