@@ -415,8 +415,12 @@ def test_geglu_band_two_blocks_per_pass_every_output_layout() -> None:
 
 
 @pytest.mark.parametrize("rows,blocks,n,wcol0,ncols,weight_offset", [
-    (1, 129, 64, 0, 64, 0),     # the first block count past 128: one block per lane, four waves along K
-    (2, 176, 2048, 0, 2048, 0),  # K = 5632 (TinyLlama down), two rows
+    (1, 129, 64, 0, 64, 0),     # one row of 129 blocks: still the split kernel (one row spreads past 512)
+    (2, 176, 2048, 0, 2048, 0),  # K = 5632 (TinyLlama down), two rows: one block per lane
+    (3, 200, 50, 0, 50, 0),     # three rows, one block per lane
+    (2, 300, 60, 1, 50, 0),     # two rows, two blocks per lane
+    (2, 600, 30, 0, 30, 0),     # two rows, three blocks per lane
+    (3, 700, 30, 0, 30, 2),     # three rows, three blocks per lane, weights 2 bytes off
     (4, 256, 100, 3, 90, 0),    # K = 8192, the last count with one block per lane
     (3, 257, 40, 0, 40, 2),     # two blocks per lane; weights 2 bytes past a 16-byte boundary
     (4, 344, 300, 10, 280, 0),  # K = 11008 (Llama-7B down), four rows
