@@ -415,7 +415,8 @@ def test_geglu_band_two_blocks_per_pass_every_output_layout() -> None:
 
 
 @pytest.mark.parametrize("rows,blocks,n,wcol0,ncols,weight_offset", [
-    (1, 129, 64, 0, 64, 0),     # one row of 129 blocks: still the split kernel (one row spreads past 512)
+    (1, 129, 64, 0, 64, 0),     # one row of 129 blocks: still the split kernel (one row spreads past 256)
+    (1, 300, 64, 0, 64, 0),     # one row, two blocks per lane
     (2, 176, 2048, 0, 2048, 0),  # K = 5632 (TinyLlama down), two rows: one block per lane
     (3, 200, 50, 0, 50, 0),     # three rows, one block per lane
     (2, 300, 60, 1, 50, 0),     # two rows, two blocks per lane
