@@ -938,7 +938,8 @@ def leg_cfg1(torch, args) -> dict:
 
 
 def leg_copy(torch) -> dict:
-    """Device-to-device copy ceiling (reads + writes) for context next to the 8 TB/s spec."""
+    """Device-to-device copy ceiling (reads + writes) and the plain streaming read rate
+    (``qxt_hbm_read_probe`` over 1 GiB), for context next to the 8 TB/s spec."""
     nbytes = 1 << 30
     src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
     dst = torch.empty_like(src)
@@ -952,9 +953,25 @@ def leg_copy(torch) -> dict:
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / 10
-    del src, dst
+    del dst
+    # Read ceiling: the library's plain streaming read of the same 1 GiB.
+    from qpu_xla_amd import _lib
+
+    partials = torch.empty(2048, dtype=torch.int32, device="cuda")
+    stream = ctypes.c_void_p(int(torch.cuda.current_stream().cuda_stream))
+    for _ in range(3):
+        _lib.call("qxt_hbm_read_probe", _p(src), nbytes, _p(partials), stream)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(10):
+        _lib.call("qxt_hbm_read_probe", _p(src), nbytes, _p(partials), stream)
+    end.record()
+    torch.cuda.synchronize()
+    read_ms = start.elapsed_time(end) / 10
+    del src, partials
     torch.cuda.empty_cache()
-    return {"bytes": 2 * nbytes, "gbs": 2 * nbytes / (ms * 1e-3) / 1e9}
+    return {"bytes": 2 * nbytes, "gbs": 2 * nbytes / (ms * 1e-3) / 1e9,
+            "read_bytes": nbytes, "read_gbs": nbytes / (read_ms * 1e-3) / 1e9}
 
 
 def cpu_baseline_q4(budget_s: float) -> dict:
@@ -1252,6 +1269,8 @@ def main() -> int:
                 "peak": PEAK_HBM_GBS,
                 "unit": "GB/s",
                 "frac": head["kernel_gbs"] / PEAK_HBM_GBS,
+                "frac_of_measured_read_rate": (head["kernel_gbs"] / out["copy"]["read_gbs"]
+                                               if out.get("copy", {}).get("read_gbs") else None),
                 "traffic": (traffic or {}).get("bytes"),
                 "traffic_source": (traffic or {}).get("source"),
                 "bytes_per_launch": head["kernel_bytes_per_launch"],
@@ -1272,6 +1291,7 @@ def main() -> int:
         "decode": decode,
         "configs": {key: out[key] for key in ("cfg0", "cfg1", "cfg2", "cfg2_native_layout") if key in out},
         "copy_ceiling_gbs": out.get("copy", {}).get("gbs"),
+        "read_ceiling_gbs": out.get("copy", {}).get("read_gbs"),
         "device": device,
     }
     print(json.dumps(line), flush=True)

@@ -116,6 +116,16 @@ typedef struct qxt_launch_record {
 int qxt_timing_begin(void);
 int qxt_timing_end(qxt_launch_record *records, uint32_t capacity, uint32_t *count);
 
+/* Measurement utility with no reference counterpart, for benchmarks: reads
+ * `bytes` (a positive multiple of 16) at `src` (16-byte aligned) once, with
+ * the fastest plain streaming pattern this library found for the device (a
+ * grid of 2048 workgroups of 256 threads, 16-byte non-temporal loads
+ * grid-stride), and stores in partials[w] the xor of the 32-bit words that
+ * workgroup w read; the xor of all 2048 partials is the xor of every word of
+ * the buffer.  Its device time over a buffer far larger than the caches is
+ * the device's achievable HBM read rate. */
+int qxt_hbm_read_probe(const void *src, size_t bytes, uint32_t *partials, void *stream);
+
 /* ------------------------------------------------------------- quantisers */
 
 /* fp32 rows x[rows, columns] -> native Q8_0 blocks u8 [rows, columns/32, 34].

@@ -160,6 +160,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "qxt_timing_end": (c_int, [POINTER(LaunchRecord), _U, POINTER(_U)]),
     "qxt_quantize_q8_0": (c_int, [_P, _SZ, _P, _SZ, _U, _U, _P]),
     "qxt_q8_0_scale_check": (c_int, [_P, _P]),
+    "qxt_hbm_read_probe": (c_int, [_P, c_size_t, _P, _P]),
     "qxt_quantize_rows_int8": (c_int, [_P, _SZ, _P, _SZ, _P, _U, _U, _U, _U, _P]),
     "qxt_quantize_q4_0": (c_int, [_P, _SZ, _P, _SZ, _U, _U, _P]),
     "qxt_ggml_gelu_fp16_table": (c_int, [_P]),

@@ -78,6 +78,8 @@ FAKE = ctypes.c_void_p(1 << 20)  # 16-byte aligned, never dereferenced: validati
         ("qxt_quantize_q8_0", (FAKE, 128, FAKE, 34, 1, 40, None), "multiple of 32"),
         ("qxt_q8_0_scale_check", (None, None), "bad counter"),
         ("qxt_q8_0_scale_check", (ctypes.c_void_p((1 << 20) + 4), None), "bad counter"),
+        ("qxt_hbm_read_probe", (None, 16, FAKE, None), "null or misaligned"),
+        ("qxt_hbm_read_probe", (FAKE, 24, FAKE, None), "multiple of 16"),
         ("qxt_quantize_rows_int8", (FAKE, 64, FAKE, 8, FAKE, 1, 16, 8, 0, None), "padded_columns"),
         ("qxt_quantize_rows_int8", (FAKE, 64, FAKE, 16, FAKE, 1, 16, 16, 8, None), "unknown flags"),
         ("qxt_ggml_q4_0_q8_0_linear", (FAKE, 34, FAKE, 18, FAKE, 64, 0, 1, 0, 0, 16, None), "positive"),

@@ -286,3 +286,19 @@ def test_geglu_producer_known_answers() -> None:
     gate = dev(np.full_like(row, 4.0))
     blocks = ggml_geglu_q8_0(gate, dev(row)).cpu().numpy()[0]
     _check_q8_0_blocks(blocks, expected, scale_shift=2)
+
+
+def test_hbm_read_probe_reads_every_word_once() -> None:
+    # The xor of the per-workgroup partials is the xor of every 32-bit word:
+    # each 16-byte chunk was read exactly once (an even count would cancel).
+    from qpu_xla_amd import _lib
+
+    rng = np.random.default_rng(77)
+    for nbytes in (16, 4096 + 48, (3 << 20) + 16 * 2047):
+        host = rng.integers(0, 2**32, size=nbytes // 4, dtype=np.uint32)
+        src = torch.from_numpy(host.view(np.int32)).to("cuda")
+        partials = torch.zeros(2048, dtype=torch.int32, device="cuda")
+        _lib.call("qxt_hbm_read_probe", ctypes.c_void_p(src.data_ptr()), nbytes, ctypes.c_void_p(partials.data_ptr()),
+                  None)
+        got = np.bitwise_xor.reduce(partials.cpu().numpy().view(np.uint32))
+        assert got == np.bitwise_xor.reduce(host)
