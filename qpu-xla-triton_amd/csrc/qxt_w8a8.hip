@@ -1190,7 +1190,14 @@ int qxt_w8a8_linear(const float *x, size_t ldx, int8_t *qa, size_t ldqa, float *
     if (x == nullptr || ldx % 4 || ldx < static_cast<size_t>(k) * 4 || !aligned(x, 4))
         return fail(QXT_INVALID_ARGUMENT, "w8a8 linear: bad activation input");
     if (flags & ~QXT_QUANT_NO_SCALE_FLOOR) return fail(QXT_INVALID_ARGUMENT, "w8a8 linear: unknown flags");
-    if (gemv_path(static_cast<int>(m), static_cast<int>(k)) && k <= 4u * kThreads * kGemvRowChunks &&
+    // Three or four rows of at most 4096 columns take the row pre-pass and the
+    // unfused GEMV instead: every fused workgroup quantises all the rows, and
+    // at K = 4096, N = 14336 (1792 workgroups) that costs more than a second
+    // launch (measured on MI355X, rotated weights: M = 4 30.3 -> 23.9 us,
+    // M = 3 26.8 -> 23.5 us; at K = 14336 the fused launch stays ahead,
+    // M = 4 22.3 against 23.5 us, and so does M = 2 at either K).
+    const bool fuse_rows = m <= 2 || k > 4096;
+    if (fuse_rows && gemv_path(static_cast<int>(m), static_cast<int>(k)) && k <= 4u * kThreads * kGemvRowChunks &&
         aligned(x, 16) && ldx % 16 == 0 &&
         static_cast<uint64_t>(m - 1) * ldx + static_cast<uint64_t>(k) * 4 < (1ull << 31)) {
         // One launch: every GEMV workgroup quantises the rows itself.

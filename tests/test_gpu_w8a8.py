@@ -150,11 +150,14 @@ def test_gemv_rows_exact_both_layouts_and_epilogue(m: int, n: int, k: int) -> No
     np.testing.assert_array_equal(y, oracle.dequantize_epilogue(expected, sa, sw, bias))
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 16, 16), (1, 4096, 14336), (2, 100, 4096), (3, 33, 2048), (4, 14336, 4096)])
+@pytest.mark.parametrize("m,n,k", [(1, 16, 16), (1, 4096, 14336), (2, 100, 4096), (3, 33, 2048), (4, 14336, 4096),
+                                   (3, 70, 4112), (4, 300, 14336)])
 @pytest.mark.parametrize("floor", [True, False])
 def test_small_m_linear_quantises_in_the_gemv_kernel_bit_exact(m: int, n: int, k: int, floor: bool) -> None:
-    # M <= 4: one launch quantises the rows inside every GEMV workgroup; the
-    # workspaces still receive the int8 rows and scales.
+    # M <= 2, or K > 4096: one launch quantises the rows inside every GEMV
+    # workgroup; three or four rows of at most 4096 columns take the row
+    # pre-pass and the unfused GEMV.  Either way the workspaces receive the
+    # int8 rows and scales.
     from qpu_xla_amd import _lib
     from qpu_xla_amd._tensors import ptr, row_stride
 
