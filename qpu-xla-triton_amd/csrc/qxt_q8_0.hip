@@ -6,12 +6,14 @@
 // unlike the Q4_0 path -- summed in block order.  The kernel reproduces that
 // result bit for bit.
 //
-// Same plan as the Q4_0 decode kernel: a workgroup owns a tile of output
-// columns; on the fast path (blocks % 8 == 0, 16-byte aligned rows) a thread
-// takes "units" of 8 consecutive blocks of one column (272 bytes = 17 x 16-byte
-// loads, issued before the activation is staged), block terms go to LDS and
-// one thread per (row, column) adds them in block order.  Otherwise a thread
-// takes one block with 2-byte loads.
+// Two forms; in both a workgroup owns a tile of output columns, block terms
+// go to LDS and one thread per (row, column) adds them in block order.  Up to
+// 512 blocks (K <= 16384) the block-per-lane form (q8_0_stream_kernel, below)
+// spreads each column's blocks over the lanes and keeps the activation in
+// registers.  Beyond it, the unit form: on its fast path (blocks % 8 == 0,
+// 16-byte aligned rows) a thread takes "units" of 8 consecutive blocks of one
+// column (272 bytes = 17 x 16-byte loads, issued before the activation is
+// staged in LDS); otherwise a thread takes one block with 2-byte loads.
 #include <algorithm>
 #include <type_traits>
 
