@@ -1606,17 +1606,16 @@ int qxt_ggml_q4_0_q8_0_linear(const void *activation, size_t activation_row_stri
         return q4_0_tiled_native(activation, activation_row_stride, weight, weight_row_stride, destination,
                                  destination_row_stride, rows, blocks, weight_column_start, output_column_start,
                                  column_count, as_stream(stream));
-    // Rows of more than 128 blocks with two or more activation rows (one row:
-    // more than 256 blocks) spread their blocks over the lanes instead
-    // (measured on MI355X, event-timed: M=4 K=5632 8.0 -> 6.5 us, K=8192
-    // 12.5 -> 9.9, K=11008 16.2 -> 14.1, K=14336 30.2 -> 14.8; M=2 K=5632
-    // 7.4 -> 5.6; one row at K=11008 / 14336 11.1 -> 10.4 / 12.7 -> 11.6 us,
-    // but at K=5632 / 8192 4.8 -> 5.5 / 6.8 -> 7.8 us, where one row keeps the
-    // split kernels).
-#ifndef QXT_Q4_STREAM_ONE_ROW
-#define QXT_Q4_STREAM_ONE_ROW 256
-#endif
-    if (blocks > (rows == 1 ? static_cast<uint32_t>(QXT_Q4_STREAM_ONE_ROW) : 128u)) {
+    // Long rows spread their blocks over the lanes instead: more than 128
+    // blocks with four or more activation rows, more than 64 with two or
+    // three, more than 256 with one (measured on MI355X, event-timed: M=4
+    // K=5632 8.0 -> 6.5 us, K=8192 12.5 -> 9.9, K=11008 16.2 -> 14.1,
+    // K=14336 30.2 -> 14.8; M=2 K=4096 10.7 -> 9.0, K=5632 7.4 -> 5.6; one row
+    // at K=11008 / 14336 11.1 -> 10.4 / 12.7 -> 11.6 us; where the other
+    // kernels stay they were ahead: M=4 K=4096 N=4096 6.1 against 6.7 us,
+    // one row at K=5632 / 8192 4.8 / 6.8 against 5.5 / 7.8 us).
+    const uint32_t spread_above = rows == 1 ? 256u : rows <= 3 ? 64u : 128u;
+    if (blocks > spread_above) {
         rc = q4_0_stream_native(activation, activation_row_stride, weight, weight_row_stride, destination,
                                 destination_row_stride, rows, blocks, weight_column_start, output_column_start,
                                 column_count, as_stream(stream));
