@@ -651,7 +651,7 @@ struct FusedRows {
     int floor;
 };
 
-// Load fp32 row r of the fused path into xv (zeros past K).
+// Load fp32 row r of the fused path into xv (zeros past K, and for r >= M).
 template <int RC, int NT = kThreads>
 __device__ __forceinline__ void load_row(const GemmArgs &args, const FusedRows &f, int r, v4u (&xv)[RC]) {
     const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(f.x, f.x_bytes);
@@ -660,7 +660,7 @@ __device__ __forceinline__ void load_row(const GemmArgs &args, const FusedRows &
 #pragma unroll
     for (int u = 0; u < RC; ++u) {
         const int c = threadIdx.x + u * NT;
-        xv[u] = __builtin_amdgcn_raw_buffer_load_b128(rx, c < k4 ? base + c * 16 : kOutOfRange, 0, 0);
+        xv[u] = __builtin_amdgcn_raw_buffer_load_b128(rx, c < k4 && r < args.m ? base + c * 16 : kOutOfRange, 0, 0);
     }
 }
 
@@ -685,6 +685,13 @@ __device__ __forceinline__ void stage_rows(const GemmArgs &args, const FusedRows
     } else {
         uint32_t *aw = reinterpret_cast<uint32_t *>(act);
         const int k4 = args.k / 4;
+        // Rows of up to 8 chunks per thread request the next row before
+        // reducing this one, so the row reads do not wait on each other
+        // (measured on MI355X, M = 2: K = 14336, N = 4096 16.0 -> 14.5 us,
+        // K = 4096, N = 14336 13.4 -> 12.6 us).
+        constexpr bool kNextRow = RC <= 8;
+        v4u xn[kNextRow ? RC : 1];
+#pragma unroll
         for (int r = 0; r < MR; ++r) {
             // Row 0 always exists (every entry point requires m >= 1).  Its
             // quantisation stays unconditional: behind an `r < m` branch the
@@ -700,9 +707,14 @@ __device__ __forceinline__ void stage_rows(const GemmArgs &args, const FusedRows
             if (r == 0) {
 #pragma unroll
                 for (int u = 0; u < RC; ++u) xv[u] = xv0[u];
+            } else if constexpr (kNextRow) {
+#pragma unroll
+                for (int u = 0; u < RC; ++u) xv[u] = xn[u];
             } else {
                 load_row<RC, NT>(args, f, r, xv);
             }
+            if constexpr (kNextRow)
+                if (r + 1 < MR) load_row<RC, NT>(args, f, r + 1, xn);
             float amax = 0.0f;
 #pragma unroll
             for (int u = 0; u < RC; ++u)
@@ -836,6 +848,100 @@ __global__ __launch_bounds__(NT) void w8a8_gemv_nk_kernel(GemmArgs args, FusedRo
 #pragma unroll
             for (int r = 0; r < MR; ++r)
                 if (n0 + j < args.n && r < args.m) store_one<EPI>(args, r, n0 + j, acc[j][r], row_sa[r]);
+    }
+}
+
+// Fused rows over [N, K] weights, persistent form: a fixed grid of
+// workgroups quantises the rows once each, then every wave walks its columns
+// gw, gw + W, gw + 2 W, ... (W waves in the grid, gw = wave * grid + block,
+// so every workgroup holds the same number of columns to within one per
+// wave) as one stream of kilobyte loads, D of them in flight across column
+// boundaries.  A wave sum ends each column; lane j keeps the sum of the
+// wave's column j and the outputs are stored after the last load (at most 64
+// columns per wave): a store between the loads would leave reads and writes
+// outstanding together, and the next wait would then drain every load in
+// flight.  Measured on MI355X (rotated weights, back-to-back launches, against
+// the one-column-per-wave kernel): M = 1, K = 4096: N = 14336 13.5 -> 11.6 us,
+// N = 11008 11.1 -> 9.7 us; M = 1, K = 2048, N = 16384 11.5 -> 7.6 us; M = 2,
+// K = 4096, N = 14336 20.0 -> 12.6 us; M = 2, K = 14336, N = 4096 16.0 ->
+// 14.5 us; one row of one column per wave (K = 14336, N = 4096) 11.8 against
+// 11.9 us, so one row takes this form from two columns per wave.  Four loads
+// in flight per wave and two workgroups per CU: eight or sixteen loads were
+// slower (12.5 / 14.4 us at M = 1, N = 14336), three workgroups per CU with
+// three loads within 0.5 us either way, four workgroups per CU slower.
+#ifndef QXT_GEMV_RING
+#define QXT_GEMV_RING 4
+#endif
+template <int MR, int RC, int EPI, int NT, int D>
+__global__ __launch_bounds__(NT) void w8a8_gemv_nk_stream_kernel(GemmArgs args, FusedRows f) {
+    extern __shared__ v4u act[];  // [MR][K / 16]
+    __shared__ float row_sa[4];
+    __shared__ float scratch[NT / 64];
+    const int k16 = args.k / 16;
+    const int chunks = (k16 + 63) / 64;  // kilobyte loads per column and lane
+    const int lane = threadIdx.x & 63;
+    const int waves = gridDim.x * (NT / 64);
+    const int gw = __builtin_amdgcn_readfirstlane((threadIdx.x >> 6) * gridDim.x + blockIdx.x);
+    const int ncols = gw < args.n ? (args.n - gw + waves - 1) / waves : 0;  // <= 64 (checked by the launch)
+    const int total = ncols * chunks;
+    const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(args.w, args.w_bytes);
+    int icol = gw, ichunk = 0;  // the next load: chunk `ichunk` of column `icol`
+    auto issue = [&](v4u &slot, int t) {
+        const int c = lane + 64 * ichunk;
+        const uint32_t off =
+            t < total && c < k16 ? static_cast<uint32_t>(icol) * args.ldw + static_cast<uint32_t>(c) * 16 : kOutOfRange;
+        slot = __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, kNonTemporal);
+        if (++ichunk == chunks) {
+            ichunk = 0;
+            icol += waves;
+        }
+    };
+    v4u xv0[RC];
+    load_row<RC, NT>(args, f, 0, xv0);
+    v4u ring[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) issue(ring[d], d);
+    stage_rows<MR, RC, true, NT>(args, f, act, row_sa, scratch, xv0);
+    int acc[MR], res[MR];
+#pragma unroll
+    for (int r = 0; r < MR; ++r) acc[r] = res[r] = 0;
+    int j = 0, chunk = 0;  // the load being reduced: chunk `chunk` of the wave's column j
+    for (int t0 = 0; t0 < total; t0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            if (t0 + d < total) {
+                const int c = lane + 64 * chunk;
+                if (c < k16) {
+#pragma unroll
+                    for (int r = 0; r < MR; ++r) {
+                        const v4u av = act[r * k16 + c];
+                        int sum = acc[r];
+                        sum = dot4(static_cast<int>(ring[d][0]), static_cast<int>(av[0]), sum);
+                        sum = dot4(static_cast<int>(ring[d][1]), static_cast<int>(av[1]), sum);
+                        sum = dot4(static_cast<int>(ring[d][2]), static_cast<int>(av[2]), sum);
+                        sum = dot4(static_cast<int>(ring[d][3]), static_cast<int>(av[3]), sum);
+                        acc[r] = sum;
+                    }
+                }
+                if (++chunk == chunks) {
+#pragma unroll
+                    for (int r = 0; r < MR; ++r) {
+                        const int s = wave_sum(acc[r]);
+                        if (lane == j) res[r] = s;
+                        acc[r] = 0;
+                    }
+                    chunk = 0;
+                    ++j;
+                }
+            }
+            issue(ring[d], t0 + d + D);
+        }
+    }
+    if (lane < ncols) {
+        const int col = gw + lane * waves;
+#pragma unroll
+        for (int r = 0; r < MR; ++r)
+            if (r < args.m) store_one<EPI>(args, r, col, res[r], row_sa[r]);
     }
 }
 
@@ -996,9 +1102,43 @@ int launch_gemv_rc(GemmArgs args, const FusedRows &f, int epi, uint32_t layout, 
 #define QXT_GEMV_WIDE 1
 #endif
 constexpr bool kGemvWide = QXT_GEMV_WIDE != 0;
+#ifndef QXT_GEMV_STREAM
+#define QXT_GEMV_STREAM 1
+#endif
+#ifndef QXT_GEMV_STREAM_WGS
+#define QXT_GEMV_STREAM_WGS 2
+#endif
+#ifndef QXT_GEMV_STREAM_ROWS
+#define QXT_GEMV_STREAM_ROWS 2
+#endif
+// The persistent form of the fused GEMV, or QXT_CAPABILITY_MISSING where the
+// one-column-per-wave kernel takes the problem: one row with fewer than two
+// columns per wave, or more than 64 columns per wave.
+template <int MR, int RC>
+int launch_gemv_stream(GemmArgs args, const FusedRows &f, int epi, hipStream_t stream) {
+    constexpr int NT = 2 * kThreads, D = QXT_GEMV_RING, kWaves = NT / 64;
+    const size_t lds = static_cast<size_t>(MR) * args.k;
+    // Workgroups resident together on a CU: at most the requested count and
+    // what 160 KB of LDS holds, so that the whole grid runs at once.
+    const long per_cu =
+        std::max<long>(1, std::min<long>(QXT_GEMV_STREAM_WGS, (160L * 1024) / static_cast<long>(lds + 1024)));
+    const long wgs = std::min<long>(per_cu * compute_units(), (static_cast<long>(args.n) + kWaves - 1) / kWaves);
+    const long waves = wgs * kWaves;
+    if ((MR == 1 && args.n < 2 * waves) || args.n > 64 * waves) return QXT_CAPABILITY_MISSING;
+    args.a_bytes = static_cast<uint32_t>(static_cast<size_t>(args.m - 1) * args.lda + args.k);
+    args.w_bytes = static_cast<uint32_t>(static_cast<size_t>(args.n - 1) * args.ldw + args.k);
+    auto kernel = epi == EPI_DEQUANT ? w8a8_gemv_nk_stream_kernel<MR, RC, EPI_DEQUANT, NT, D>
+                                     : w8a8_gemv_nk_stream_kernel<MR, RC, EPI_DEQUANT_BIAS, NT, D>;
+    return launch("w8a8_gemv_kernel", kernel, dim3(static_cast<uint32_t>(wgs)), dim3(NT), lds, stream, args, f);
+}
 template <int MR, bool FUSED>
 int launch_gemv(const GemmArgs &args, const FusedRows &f, int epi, uint32_t layout, hipStream_t stream) {
     if constexpr (FUSED) {
+        if (QXT_GEMV_STREAM && MR <= QXT_GEMV_STREAM_ROWS && layout == QXT_W8A8_WEIGHT_NK && epi != EPI_I32) {
+            const int rc = args.k <= 4 * 4 * 2 * kThreads ? launch_gemv_stream<MR, 4>(args, f, epi, stream)
+                                                          : launch_gemv_stream<MR, 8>(args, f, epi, stream);
+            if (rc != QXT_CAPABILITY_MISSING) return rc;
+        }
         if (kGemvWide && layout == QXT_W8A8_WEIGHT_NK) {
             constexpr int NT = 2 * kThreads;
             if (args.k <= 4 * 4 * NT) return launch_gemv_rc<MR, 4, true, NT>(args, f, epi, layout, stream);

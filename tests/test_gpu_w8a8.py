@@ -424,7 +424,7 @@ def test_calibrated_auto_selects_the_fastest_exact_partition_axis() -> None:
 
 
 @pytest.mark.parametrize("layout", ["nk", "k4n"])
-@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("m", [1, 2, 4])
 @pytest.mark.parametrize("k", [8192, 8208, 16384])
 def test_fused_rows_at_register_chunk_boundaries_bit_exact(layout: str, m: int, k: int) -> None:
     # The fused row quantiser holds K / (4 NT) 16-byte chunks per thread: K =
@@ -467,6 +467,63 @@ def test_fused_rows_at_register_chunk_boundaries_bit_exact(layout: str, m: int, 
         assert int(got_s[r : r + 1].view(np.uint32)[0]) == scale_bits
     expected = oracle.dequantize_epilogue(oracle.int8_gemm_i32(qa_ref, qw), sa_ref, sw, bias)
     np.testing.assert_array_equal(y.cpu().numpy(), expected)
+
+
+def _fused_case(m: int, n: int, k: int, bias: bool, seed: int) -> None:
+    from qpu_xla_amd import _lib
+    from qpu_xla_amd._tensors import ptr, row_stride
+
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    x[:, rng.choice(k, max(1, k // 1000), replace=False)] *= 20.0
+    qw = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    sw = rng.uniform(0.0005, 0.002, n).astype(np.float32)
+    b = rng.standard_normal(n, dtype=np.float32) if bias else None
+    xd, w_d, sw_d = dev(x), dev(qw), dev(sw)
+    b_d = dev(b) if bias else None
+    qa = torch.full((m, k), 99, dtype=torch.int8, device="cuda")
+    sa = torch.full((m,), -1.0, dtype=torch.float32, device="cuda")
+    y = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+    _lib.call("qxt_w8a8_linear", ptr(xd), row_stride(xd), ptr(qa), row_stride(qa), ptr(sa), ptr(w_d), row_stride(w_d),
+              ptr(sw_d), ptr(b_d) if bias else None, ptr(y), row_stride(y), m, n, k, _lib.WEIGHT_NK, 0, None)
+    torch.cuda.synchronize()
+    qa_ref, sa_ref = oracle.quantize_rows_int8(x)
+    np.testing.assert_array_equal(qa.cpu().numpy(), qa_ref)
+    np.testing.assert_array_equal(sa.cpu().numpy(), sa_ref)
+    expected = oracle.dequantize_epilogue(oracle.int8_gemm_i32(qa_ref, qw), sa_ref, sw, b)
+    np.testing.assert_array_equal(y.cpu().numpy(), expected)
+
+
+# Column counts in units of the persistent form's waves: two 512-thread
+# workgroups per CU, eight waves each.
+def _waves() -> int:
+    return 16 * torch.cuda.get_device_properties(0).multi_processor_count
+
+
+@pytest.mark.parametrize("m,cols,k", [
+    (1, (2, 0), 16),      # one row: exactly two columns per wave, one 16-byte chunk per column
+    (1, (2, 3), 4112),    # ragged: a partial last kilobyte, three waves with a third column
+    (1, (2, -1), 2048),   # one column short of two per wave: the one-column-per-wave kernel
+    (1, (3, 1000), 4096),  # three or four columns per wave
+    (1, (2, 5), 8208),    # rows of more than 8192 columns: eight row chunks per thread
+    (1, (64, 0), 16),     # 64 columns per wave, the most the persistent form holds
+    (1, (64, 1), 16),     # one more: the one-column-per-wave kernel
+    (2, (0, 100), 4096),  # two rows: a grid of 13 workgroups, most waves without a column
+    (2, (0, 3000), 4112),
+    (2, (0, 520), 16384),  # the longest fused row
+    (2, (0, 4096), 14336),
+    (2, (64, 0), 16),
+    (2, (64, 1), 16),
+])
+@pytest.mark.parametrize("bias", [True, False])
+def test_fused_gemv_persistent_form_bit_exact(m: int, cols: tuple, k: int, bias: bool) -> None:
+    # One or two fused rows over [N, K] weights: each workgroup quantises the
+    # rows once, then every wave streams its columns gw, gw + W, ... with four
+    # kilobyte loads in flight across column boundaries and stores them after
+    # the last load.  N = per_wave * W + extra.
+    per_wave, extra = cols
+    n = per_wave * _waves() + extra
+    _fused_case(m, n, k, bias, seed=8100 + m * 7 + k + per_wave)
 
 
 def _int8_case(seed: int, m: int, n: int, k: int):
