@@ -868,7 +868,9 @@ __global__ __launch_bounds__(NT) void w8a8_gemv_nk_kernel(GemmArgs args, FusedRo
 // 11.9 us, so one row takes this form from two columns per wave.  Four loads
 // in flight per wave and two workgroups per CU: eight or sixteen loads were
 // slower (12.5 / 14.4 us at M = 1, N = 14336), three workgroups per CU with
-// three loads within 0.5 us either way, four workgroups per CU slower.
+// three loads within 0.5 us either way, four workgroups per CU slower, and
+// 1024-thread workgroups (one or two per CU) slower at every shape measured
+// (M = 1, K = 14336, N = 4096 11.7 -> 12.4-12.8 us).
 #ifndef QXT_GEMV_RING
 #define QXT_GEMV_RING 4
 #endif
@@ -1111,12 +1113,18 @@ constexpr bool kGemvWide = QXT_GEMV_WIDE != 0;
 #ifndef QXT_GEMV_STREAM_ROWS
 #define QXT_GEMV_STREAM_ROWS 2
 #endif
+#ifndef QXT_GEMV_STREAM_NT
+#define QXT_GEMV_STREAM_NT 512
+#endif
+#ifndef QXT_GEMV_STREAM_MIN_COLS
+#define QXT_GEMV_STREAM_MIN_COLS 2
+#endif
 // The persistent form of the fused GEMV, or QXT_CAPABILITY_MISSING where the
 // one-column-per-wave kernel takes the problem: one row with fewer than two
 // columns per wave, or more than 64 columns per wave.
 template <int MR, int RC>
 int launch_gemv_stream(GemmArgs args, const FusedRows &f, int epi, hipStream_t stream) {
-    constexpr int NT = 2 * kThreads, D = QXT_GEMV_RING, kWaves = NT / 64;
+    constexpr int NT = QXT_GEMV_STREAM_NT, D = QXT_GEMV_RING, kWaves = NT / 64;
     const size_t lds = static_cast<size_t>(MR) * args.k;
     // Workgroups resident together on a CU: at most the requested count and
     // what 160 KB of LDS holds, so that the whole grid runs at once.
@@ -1124,7 +1132,7 @@ int launch_gemv_stream(GemmArgs args, const FusedRows &f, int epi, hipStream_t s
         std::max<long>(1, std::min<long>(QXT_GEMV_STREAM_WGS, (160L * 1024) / static_cast<long>(lds + 1024)));
     const long wgs = std::min<long>(per_cu * compute_units(), (static_cast<long>(args.n) + kWaves - 1) / kWaves);
     const long waves = wgs * kWaves;
-    if ((MR == 1 && args.n < 2 * waves) || args.n > 64 * waves) return QXT_CAPABILITY_MISSING;
+    if ((MR == 1 && args.n < QXT_GEMV_STREAM_MIN_COLS * waves) || args.n > 64 * waves) return QXT_CAPABILITY_MISSING;
     args.a_bytes = static_cast<uint32_t>(static_cast<size_t>(args.m - 1) * args.lda + args.k);
     args.w_bytes = static_cast<uint32_t>(static_cast<size_t>(args.n - 1) * args.ldw + args.k);
     auto kernel = epi == EPI_DEQUANT ? w8a8_gemv_nk_stream_kernel<MR, RC, EPI_DEQUANT, NT, D>
@@ -1135,7 +1143,7 @@ template <int MR, bool FUSED>
 int launch_gemv(const GemmArgs &args, const FusedRows &f, int epi, uint32_t layout, hipStream_t stream) {
     if constexpr (FUSED) {
         if (QXT_GEMV_STREAM && MR <= QXT_GEMV_STREAM_ROWS && layout == QXT_W8A8_WEIGHT_NK && epi != EPI_I32) {
-            const int rc = args.k <= 4 * 4 * 2 * kThreads ? launch_gemv_stream<MR, 4>(args, f, epi, stream)
+            const int rc = args.k <= 4 * 4 * QXT_GEMV_STREAM_NT ? launch_gemv_stream<MR, 4>(args, f, epi, stream)
                                                           : launch_gemv_stream<MR, 8>(args, f, epi, stream);
             if (rc != QXT_CAPABILITY_MISSING) return rc;
         }
