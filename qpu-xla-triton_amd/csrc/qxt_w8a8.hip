@@ -851,8 +851,9 @@ __global__ __launch_bounds__(NT) void w8a8_gemv_nk_kernel(GemmArgs args, FusedRo
     }
 }
 
-// Fused rows over [N, K] weights, persistent form: a fixed grid of
-// workgroups quantises the rows once each, then every wave walks its columns
+// Rows over [N, K] weights, persistent form: a fixed grid of workgroups
+// stages the rows once each (quantising fp32 rows in the fused linear,
+// loading int8 rows otherwise), then every wave walks its columns
 // gw, gw + W, gw + 2 W, ... (W waves in the grid, gw = wave * grid + block,
 // so every workgroup holds the same number of columns to within one per
 // wave) as one stream of kilobyte loads, D of them in flight across column
@@ -870,11 +871,17 @@ __global__ __launch_bounds__(NT) void w8a8_gemv_nk_kernel(GemmArgs args, FusedRo
 // slower (12.5 / 14.4 us at M = 1, N = 14336), three workgroups per CU with
 // three loads within 0.5 us either way, four workgroups per CU slower, and
 // 1024-thread workgroups (one or two per CU) slower at every shape measured
-// (M = 1, K = 14336, N = 4096 11.7 -> 12.4-12.8 us).
+// (M = 1, K = 14336, N = 4096 11.7 -> 12.4-12.8 us).  Unfused (int8 rows
+// given, one to four rows), three workgroups per CU and three loads in
+// flight, against the one-row-chunk kernel: M = 1, K = 4096, N = 14336
+// 14.6 -> 11.0 us; M = 1, K = 14336, N = 4096 13.1 -> 11.9 us; M = 2, K =
+// 4096, N = 14336 16.5 -> 11.6 us; M = 4 20.4 -> 13.5 us (N = 14336) and
+// 17.2 -> 14.0 us (K = 14336, N = 4096); M = 1, K = 2048, N = 5632 6.3 ->
+// 6.0-6.2 us (two workgroups and four loads: within 0.6 us of these).
 #ifndef QXT_GEMV_RING
 #define QXT_GEMV_RING 4
 #endif
-template <int MR, int RC, int EPI, int NT, int D>
+template <int MR, int RC, int EPI, int NT, int D, bool FUSED>
 __global__ __launch_bounds__(NT) void w8a8_gemv_nk_stream_kernel(GemmArgs args, FusedRows f) {
     extern __shared__ v4u act[];  // [MR][K / 16]
     __shared__ float row_sa[4];
@@ -899,11 +906,11 @@ __global__ __launch_bounds__(NT) void w8a8_gemv_nk_stream_kernel(GemmArgs args, 
         }
     };
     v4u xv0[RC];
-    load_row<RC, NT>(args, f, 0, xv0);
+    if constexpr (FUSED) load_row<RC, NT>(args, f, 0, xv0);
     v4u ring[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) issue(ring[d], d);
-    stage_rows<MR, RC, true, NT>(args, f, act, row_sa, scratch, xv0);
+    stage_rows<MR, RC, FUSED, NT>(args, f, act, row_sa, scratch, xv0);
     int acc[MR], res[MR];
 #pragma unroll
     for (int r = 0; r < MR; ++r) acc[r] = res[r] = 0;
@@ -1119,32 +1126,50 @@ constexpr bool kGemvWide = QXT_GEMV_WIDE != 0;
 #ifndef QXT_GEMV_STREAM_MIN_COLS
 #define QXT_GEMV_STREAM_MIN_COLS 2
 #endif
+#ifndef QXT_GEMV_STREAM_UNFUSED_ROWS
+#define QXT_GEMV_STREAM_UNFUSED_ROWS 4
+#endif
+#ifndef QXT_GEMV_STREAM_MIN_COLS_UNFUSED
+#define QXT_GEMV_STREAM_MIN_COLS_UNFUSED 0
+#endif
+#ifndef QXT_GEMV_STREAM_WGS_UNFUSED
+#define QXT_GEMV_STREAM_WGS_UNFUSED 3
+#endif
+#ifndef QXT_GEMV_RING_UNFUSED
+#define QXT_GEMV_RING_UNFUSED 3
+#endif
+
 // The persistent form of the fused GEMV, or QXT_CAPABILITY_MISSING where the
 // one-column-per-wave kernel takes the problem: one row with fewer than two
 // columns per wave, or more than 64 columns per wave.
-template <int MR, int RC>
+template <int MR, int RC, bool FUSED>
 int launch_gemv_stream(GemmArgs args, const FusedRows &f, int epi, hipStream_t stream) {
-    constexpr int NT = QXT_GEMV_STREAM_NT, D = QXT_GEMV_RING, kWaves = NT / 64;
+    constexpr int NT = QXT_GEMV_STREAM_NT, kWaves = NT / 64;
+    constexpr int D = FUSED ? QXT_GEMV_RING : QXT_GEMV_RING_UNFUSED;
+    constexpr long kPerCu = FUSED ? QXT_GEMV_STREAM_WGS : QXT_GEMV_STREAM_WGS_UNFUSED;
     const size_t lds = static_cast<size_t>(MR) * args.k;
     // Workgroups resident together on a CU: at most the requested count and
     // what 160 KB of LDS holds, so that the whole grid runs at once.
     const long per_cu =
-        std::max<long>(1, std::min<long>(QXT_GEMV_STREAM_WGS, (160L * 1024) / static_cast<long>(lds + 1024)));
+        std::max<long>(1, std::min<long>(kPerCu, (160L * 1024) / static_cast<long>(lds + 1024)));
     const long wgs = std::min<long>(per_cu * compute_units(), (static_cast<long>(args.n) + kWaves - 1) / kWaves);
     const long waves = wgs * kWaves;
-    if ((MR == 1 && args.n < QXT_GEMV_STREAM_MIN_COLS * waves) || args.n > 64 * waves) return QXT_CAPABILITY_MISSING;
+    const long min_cols = MR == 1 ? (FUSED ? QXT_GEMV_STREAM_MIN_COLS : QXT_GEMV_STREAM_MIN_COLS_UNFUSED) : 0;
+    if (args.n < min_cols * waves || args.n > 64 * waves) return QXT_CAPABILITY_MISSING;
     args.a_bytes = static_cast<uint32_t>(static_cast<size_t>(args.m - 1) * args.lda + args.k);
     args.w_bytes = static_cast<uint32_t>(static_cast<size_t>(args.n - 1) * args.ldw + args.k);
-    auto kernel = epi == EPI_DEQUANT ? w8a8_gemv_nk_stream_kernel<MR, RC, EPI_DEQUANT, NT, D>
-                                     : w8a8_gemv_nk_stream_kernel<MR, RC, EPI_DEQUANT_BIAS, NT, D>;
+    auto kernel = epi == EPI_DEQUANT ? w8a8_gemv_nk_stream_kernel<MR, RC, EPI_DEQUANT, NT, D, FUSED>
+                                     : w8a8_gemv_nk_stream_kernel<MR, RC, EPI_DEQUANT_BIAS, NT, D, FUSED>;
+    if constexpr (!FUSED)
+        if (epi == EPI_I32) kernel = w8a8_gemv_nk_stream_kernel<MR, RC, EPI_I32, NT, D, FUSED>;
     return launch("w8a8_gemv_kernel", kernel, dim3(static_cast<uint32_t>(wgs)), dim3(NT), lds, stream, args, f);
 }
 template <int MR, bool FUSED>
 int launch_gemv(const GemmArgs &args, const FusedRows &f, int epi, uint32_t layout, hipStream_t stream) {
     if constexpr (FUSED) {
         if (QXT_GEMV_STREAM && MR <= QXT_GEMV_STREAM_ROWS && layout == QXT_W8A8_WEIGHT_NK && epi != EPI_I32) {
-            const int rc = args.k <= 4 * 4 * QXT_GEMV_STREAM_NT ? launch_gemv_stream<MR, 4>(args, f, epi, stream)
-                                                          : launch_gemv_stream<MR, 8>(args, f, epi, stream);
+            const int rc = args.k <= 4 * 4 * QXT_GEMV_STREAM_NT ? launch_gemv_stream<MR, 4, true>(args, f, epi, stream)
+                                                                : launch_gemv_stream<MR, 8, true>(args, f, epi, stream);
             if (rc != QXT_CAPABILITY_MISSING) return rc;
         }
         if (kGemvWide && layout == QXT_W8A8_WEIGHT_NK) {
@@ -1156,6 +1181,10 @@ int launch_gemv(const GemmArgs &args, const FusedRows &f, int epi, uint32_t layo
         if (args.k <= 8 * 4 * kThreads) return launch_gemv_rc<MR, 8, true>(args, f, epi, layout, stream);
         return launch_gemv_rc<MR, kGemvRowChunks, true>(args, f, epi, layout, stream);
     } else {
+        if (QXT_GEMV_STREAM && MR <= QXT_GEMV_STREAM_UNFUSED_ROWS && layout == QXT_W8A8_WEIGHT_NK) {
+            const int rc = launch_gemv_stream<MR, 1, false>(args, f, epi, stream);
+            if (rc != QXT_CAPABILITY_MISSING) return rc;
+        }
         return launch_gemv_rc<MR, 1, false>(args, f, epi, layout, stream);
     }
 }
@@ -1338,13 +1367,15 @@ int qxt_w8a8_linear(const float *x, size_t ldx, int8_t *qa, size_t ldqa, float *
     if (x == nullptr || ldx % 4 || ldx < static_cast<size_t>(k) * 4 || !aligned(x, 4))
         return fail(QXT_INVALID_ARGUMENT, "w8a8 linear: bad activation input");
     if (flags & ~QXT_QUANT_NO_SCALE_FLOOR) return fail(QXT_INVALID_ARGUMENT, "w8a8 linear: unknown flags");
-    // Three or four rows of at most 4096 columns take the row pre-pass and the
-    // unfused GEMV instead: every fused workgroup quantises all the rows, and
-    // at K = 4096, N = 14336 (1792 workgroups) that costs more than a second
-    // launch (measured on MI355X, rotated weights: M = 4 30.3 -> 23.9 us,
-    // M = 3 26.8 -> 23.5 us; at K = 14336 the fused launch stays ahead,
-    // M = 4 22.3 against 23.5 us, and so does M = 2 at either K).
-    const bool fuse_rows = m <= 2 || k > 4096;
+    // Three or four rows take the row pre-pass and the unfused GEMV (its
+    // persistent form) instead of quantising every row in every workgroup,
+    // except for rows longer than 4096 over at most 48 MiB of weights, where
+    // the fused launch stays ahead.  Measured on MI355X, rotated weights, back
+    // to back: M = 4, K = 4096, N = 14336 16.8 against 27.6 us fused; M = 4,
+    // K = 14336, N = 4096 20.0 against 21.8 us; M = 4, K = N = 8192 19.0
+    // against 24.3 us; M = 4, K = 11008, N = 4096 19.0 against 18.6 us; M = 3,
+    // K = 5632, N = 2048 9.9 against 8.6 us.  Two rows always fuse.
+    const bool fuse_rows = m <= 2 || (k > 4096 && static_cast<uint64_t>(n) * k <= (48ull << 20));
     if (fuse_rows && gemv_path(static_cast<int>(m), static_cast<int>(k)) && k <= 4u * kThreads * kGemvRowChunks &&
         aligned(x, 16) && ldx % 16 == 0 &&
         static_cast<uint64_t>(m - 1) * ldx + static_cast<uint64_t>(k) * 4 < (1ull << 31)) {

@@ -151,13 +151,13 @@ def test_gemv_rows_exact_both_layouts_and_epilogue(m: int, n: int, k: int) -> No
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 16, 16), (1, 4096, 14336), (2, 100, 4096), (3, 33, 2048), (4, 14336, 4096),
-                                   (3, 70, 4112), (4, 300, 14336)])
+                                   (3, 70, 4112), (4, 300, 14336), (3, 4096, 14336)])
 @pytest.mark.parametrize("floor", [True, False])
 def test_small_m_linear_quantises_in_the_gemv_kernel_bit_exact(m: int, n: int, k: int, floor: bool) -> None:
-    # M <= 2, or K > 4096: one launch quantises the rows inside every GEMV
-    # workgroup; three or four rows of at most 4096 columns take the row
-    # pre-pass and the unfused GEMV.  Either way the workspaces receive the
-    # int8 rows and scales.
+    # M <= 2, or K > 4096 over at most 48 MiB of weights: one launch
+    # quantises the rows inside every GEMV workgroup; other three- or four-row
+    # problems take the row pre-pass and the unfused GEMV.  Either way the
+    # workspaces receive the int8 rows and scales.
     from qpu_xla_amd import _lib
     from qpu_xla_amd._tensors import ptr, row_stride
 
@@ -524,6 +524,50 @@ def test_fused_gemv_persistent_form_bit_exact(m: int, cols: tuple, k: int, bias:
     per_wave, extra = cols
     n = per_wave * _waves() + extra
     _fused_case(m, n, k, bias, seed=8100 + m * 7 + k + per_wave)
+
+
+@pytest.mark.parametrize("m,cols,k", [
+    (1, (0, 7), 16),        # fewer columns than waves: a grid of one workgroup
+    (1, (2, 3), 4112),      # ragged K: a partial last kilobyte
+    (3, (0, 5000), 4096),
+    (4, (0, 4096), 14336),  # four rows of 14 KB: two workgroups per CU fit the LDS
+    (2, (1, 0), 8208),
+    (4, (64, 0), 16),       # 64 columns per wave, the most the persistent form holds
+    (4, (64, 1), 16),       # one more: the one-row-chunk kernel
+])
+@pytest.mark.parametrize("epilogue", ["i32", "dequantize", "dequantize_bias"])
+def test_unfused_gemv_persistent_form_bit_exact(m: int, cols: tuple, k: int, epilogue: str) -> None:
+    # Int8 rows given (qxt_w8a8_gemm_i32 / _dequantize at M <= 4): three
+    # workgroups per CU load the rows once each, then every wave streams its
+    # columns with three kilobyte loads in flight.  N = per_wave * W + extra,
+    # W = 24 waves per CU.
+    from qpu_xla_amd import _lib
+    from qpu_xla_amd._tensors import ptr, row_stride
+
+    per_wave, extra = cols
+    n = per_wave * 24 * torch.cuda.get_device_properties(0).multi_processor_count + extra
+    rng = np.random.default_rng(9100 + m * 13 + k + per_wave)
+    a = rng.integers(-127, 128, size=(m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    expected = oracle.int8_gemm_i32(a, w)
+    a_d, w_d = dev(a), dev(w)
+    if epilogue == "i32":
+        out = torch.full((m, n), -7, dtype=torch.int32, device="cuda")
+        _lib.call("qxt_w8a8_gemm_i32", ptr(a_d), row_stride(a_d), ptr(w_d), row_stride(w_d), ptr(out),
+                  row_stride(out), m, n, k, _lib.WEIGHT_NK, None)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(out.cpu().numpy(), expected)
+        return
+    sa = rng.uniform(0.001, 0.1, m).astype(np.float32)
+    sw = rng.uniform(0.001, 0.1, n).astype(np.float32)
+    bias = rng.standard_normal(n, dtype=np.float32) if epilogue == "dequantize_bias" else None
+    sa_d, sw_d = dev(sa), dev(sw)
+    b_d = dev(bias) if bias is not None else None
+    y = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+    _lib.call("qxt_w8a8_gemm_dequantize", ptr(a_d), row_stride(a_d), ptr(w_d), row_stride(w_d), ptr(sa_d), ptr(sw_d),
+              ptr(b_d) if b_d is not None else None, ptr(y), row_stride(y), m, n, k, _lib.WEIGHT_NK, None)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(y.cpu().numpy(), oracle.dequantize_epilogue(expected, sa, sw, bias))
 
 
 def _int8_case(seed: int, m: int, n: int, k: int):
