@@ -1606,15 +1606,21 @@ int qxt_ggml_q4_0_q8_0_linear(const void *activation, size_t activation_row_stri
         return q4_0_tiled_native(activation, activation_row_stride, weight, weight_row_stride, destination,
                                  destination_row_stride, rows, blocks, weight_column_start, output_column_start,
                                  column_count, as_stream(stream));
-    // Long rows spread their blocks over the lanes instead: more than 128
-    // blocks with four or more activation rows, more than 64 with two or
-    // three, more than 256 with one (measured on MI355X, event-timed: M=4
+    // Long rows spread their blocks over the lanes instead: more than 64
+    // blocks with two or more activation rows (128 for four rows over fewer
+    // than 8192 columns), more than 256 with one (measured on MI355X, event-timed: M=4
     // K=5632 8.0 -> 6.5 us, K=8192 12.5 -> 9.9, K=11008 16.2 -> 14.1,
     // K=14336 30.2 -> 14.8; M=2 K=4096 10.7 -> 9.0, K=5632 7.4 -> 5.6; one row
     // at K=11008 / 14336 11.1 -> 10.4 / 12.7 -> 11.6 us; where the other
     // kernels stay they were ahead: M=4 K=4096 N=4096 6.1 against 6.7 us,
     // one row at K=5632 / 8192 4.8 / 6.8 against 5.5 / 7.8 us).
-    const uint32_t spread_above = rows == 1 ? 256u : rows <= 3 ? 64u : 128u;
+    // Four rows over fewer than 8192 columns keep the matrix-core kernels up to
+    // 128 blocks; five or more rows, and four over wider outputs, spread from
+    // 65 blocks (M=4 K=4096: N=11008 10.0 -> 9.6 us, N=14336 13.3 -> 12.0 us,
+    // N=8192 9.0 -> 8.4 us; M=5 / 8 K=4096 N=11008 20.6 / 20.6 -> 17.1 / 16.5
+    // us; M=12 K=4096 N=4096 14.9 -> 10.2 us; M=5 / 8 N=4096 8.0 / 8.4 ->
+    // 7.8 / 8.2 us; from 33 blocks, M=6 and 8 at K=2048 were no faster).
+    const uint32_t spread_above = rows == 1 ? 256u : (rows != 4 || column_count >= 8192u) ? 64u : 128u;
     if (blocks > spread_above) {
         rc = q4_0_stream_native(activation, activation_row_stride, weight, weight_row_stride, destination,
                                 destination_row_stride, rows, blocks, weight_column_start, output_column_start,

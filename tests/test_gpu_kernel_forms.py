@@ -417,6 +417,10 @@ def test_geglu_band_two_blocks_per_pass_every_output_layout() -> None:
 @pytest.mark.parametrize("rows,blocks,n,wcol0,ncols,weight_offset", [
     (2, 65, 40, 0, 40, 0),      # two rows spread past 64 blocks
     (3, 64, 40, 0, 40, 0),      # three rows of 64 blocks: still the unit kernels
+    (4, 65, 8192, 0, 8192, 0),  # four rows over 8192 columns spread past 64 blocks
+    (4, 65, 8191, 0, 8191, 0),  # one column fewer: the unit kernels
+    (5, 65, 40, 0, 40, 0),      # five rows spread past 64 blocks
+    (12, 100, 50, 3, 40, 0),    # twelve rows: a second row group of four
     (1, 129, 64, 0, 64, 0),     # one row of 129 blocks: still the split kernel (one row spreads past 256)
     (1, 300, 64, 0, 64, 0),     # one row, two blocks per lane
     (2, 176, 2048, 0, 2048, 0),  # K = 5632 (TinyLlama down), two rows: one block per lane
@@ -434,8 +438,9 @@ def test_geglu_band_two_blocks_per_pass_every_output_layout() -> None:
 ])
 def test_q4_0_native_linear_long_rows_blocks_spread_over_lanes(rows: int, blocks: int, n: int, wcol0: int, ncols: int,
                                                                weight_offset: int) -> None:
-    # Native Q4_0 rows longer than 128 blocks (64 with two or three activation
-    # rows, 256 with one) and up to 15 activation rows: each lane takes
+    # Native Q4_0 rows longer than 64 blocks (128 for four activation rows
+    # over fewer than 8192 columns, 256 for one row) and up to 15 activation
+    # rows: each lane takes
     # blocks kw * 64 + l (+ 256, + 512), the activation blocks and -8 * sum(a)
     # in registers; the block terms are summed in block order.
     rng = np.random.default_rng(5600 + rows * 7 + blocks)
