@@ -570,6 +570,40 @@ def test_unfused_gemv_persistent_form_bit_exact(m: int, cols: tuple, k: int, epi
     np.testing.assert_array_equal(y.cpu().numpy(), oracle.dequantize_epilogue(expected, sa, sw, bias))
 
 
+@pytest.mark.parametrize("m,n,k", [(1, 9000, 4096), (2, 3000, 4112), (4, 9000, 4096), (3, 6000, 14336)])
+def test_small_m_linear_padded_rows_bit_exact(m: int, n: int, k: int) -> None:
+    # Row strides past the rows on every operand (fp32 input, int8 workspace,
+    # weight, output): the persistent GEMV forms (fused for one and two rows,
+    # over the pre-pass's int8 rows for three and four) address each row
+    # through its stride.
+    from qpu_xla_amd import _lib
+    from qpu_xla_amd._tensors import ptr, row_stride
+
+    rng = np.random.default_rng(9300 + m + k)
+    x_full = rng.standard_normal((m, k + 20), dtype=np.float32)
+    w_full = rng.integers(-127, 128, size=(n, k + 48), dtype=np.int8)
+    x, qw = x_full[:, :k], w_full[:, :k]
+    sw = rng.uniform(0.0005, 0.002, n).astype(np.float32)
+    bias = rng.standard_normal(n, dtype=np.float32)
+    xd, wd = dev(x_full), dev(w_full)
+    qa_full = torch.full((m, k + 32), 99, dtype=torch.int8, device="cuda")
+    sa = torch.full((m,), -1.0, dtype=torch.float32, device="cuda")
+    y_full = torch.full((m, n + 5), float("nan"), dtype=torch.float32, device="cuda")
+    sw_d, b_d = dev(sw), dev(bias)
+    _lib.call("qxt_w8a8_linear", ptr(xd), row_stride(xd), ptr(qa_full), row_stride(qa_full), ptr(sa), ptr(wd),
+              row_stride(wd), ptr(sw_d), ptr(b_d), ptr(y_full), row_stride(y_full), m, n, k, _lib.WEIGHT_NK, 0, None)
+    torch.cuda.synchronize()
+    qa_ref, sa_ref = oracle.quantize_rows_int8(np.ascontiguousarray(x))
+    got_q = qa_full.cpu().numpy()
+    np.testing.assert_array_equal(got_q[:, :k], qa_ref)
+    np.testing.assert_array_equal(got_q[:, k:], 99)
+    np.testing.assert_array_equal(sa.cpu().numpy(), sa_ref)
+    got_y = y_full.cpu().numpy()
+    expected = oracle.dequantize_epilogue(oracle.int8_gemm_i32(qa_ref, np.ascontiguousarray(qw)), sa_ref, sw, bias)
+    np.testing.assert_array_equal(got_y[:, :n], expected)
+    assert np.isnan(got_y[:, n:]).all()
+
+
 def _int8_case(seed: int, m: int, n: int, k: int):
     rng = np.random.default_rng(seed)
     a = rng.integers(-127, 128, size=(m, k), dtype=np.int8)
