@@ -420,7 +420,9 @@ def test_geglu_band_two_blocks_per_pass_every_output_layout() -> None:
     (4, 65, 8192, 0, 8192, 0),  # four rows over 8192 columns spread past 64 blocks
     (4, 65, 8191, 0, 8191, 0),  # one column fewer: the unit kernels
     (5, 65, 40, 0, 40, 0),      # five rows spread past 64 blocks
-    (12, 100, 50, 3, 40, 0),    # twelve rows: a second row group of four
+    (12, 100, 50, 3, 40, 0),    # twelve rows: row groups of four
+    (15, 130, 30, 0, 30, 2),    # fifteen rows, the most: a last row group of three; weights 2 bytes off
+    (2, 65, 1, 0, 1, 0),        # one column
     (1, 129, 64, 0, 64, 0),     # one row of 129 blocks: still the split kernel (one row spreads past 256)
     (1, 300, 64, 0, 64, 0),     # one row, two blocks per lane
     (2, 176, 2048, 0, 2048, 0),  # K = 5632 (TinyLlama down), two rows: one block per lane
