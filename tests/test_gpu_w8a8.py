@@ -2,6 +2,8 @@
 
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -602,6 +604,44 @@ def test_small_m_linear_padded_rows_bit_exact(m: int, n: int, k: int) -> None:
     expected = oracle.dequantize_epilogue(oracle.int8_gemm_i32(qa_ref, np.ascontiguousarray(qw)), sa_ref, sw, bias)
     np.testing.assert_array_equal(got_y[:, :n], expected)
     assert np.isnan(got_y[:, n:]).all()
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 14336, 4096), (2, 4096, 14336), (4, 9000, 4096)])
+def test_small_m_linear_graph_replays_bit_exact(m: int, n: int, k: int) -> None:
+    # The persistent GEMV forms captured in a HIP graph (for four rows: the row
+    # pre-pass and the GEMV over its int8 rows) and replayed three times, the
+    # outputs and the int8 workspaces cleared by eager work between replays.
+    from qpu_xla_amd import _lib
+    from qpu_xla_amd._tensors import ptr, row_stride
+
+    rng = np.random.default_rng(9400 + m)
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    qw = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    sw = rng.uniform(0.0005, 0.002, n).astype(np.float32)
+    bias = rng.standard_normal(n, dtype=np.float32)
+    qa_ref, sa_ref = oracle.quantize_rows_int8(x)
+    want = oracle.dequantize_epilogue(oracle.int8_gemm_i32(qa_ref, qw), sa_ref, sw, bias)
+    xd, wd, sw_d, b_d = dev(x), dev(qw), dev(sw), dev(bias)
+    qa = torch.empty((m, k), dtype=torch.int8, device="cuda")
+    sa = torch.empty((m,), dtype=torch.float32, device="cuda")
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    capture = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=capture):
+        _lib.call("qxt_w8a8_linear", ptr(xd), row_stride(xd), ptr(qa), row_stride(qa), ptr(sa), ptr(wd),
+                  row_stride(wd), ptr(sw_d), ptr(b_d), ptr(y), row_stride(y), m, n, k, _lib.WEIGHT_NK, 0,
+                  ctypes.c_void_p(capture.cuda_stream))
+    for _ in range(3):
+        y.fill_(float("nan"))
+        qa.fill_(99)
+        sa.fill_(-1.0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(qa.cpu().numpy(), qa_ref)
+        np.testing.assert_array_equal(sa.cpu().numpy(), sa_ref)
+        np.testing.assert_array_equal(y.cpu().numpy(), want)
 
 
 def _int8_case(seed: int, m: int, n: int, k: int):
